@@ -1,0 +1,17 @@
+// Host launchers for the gfx950 kernels (defined in kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "conv_args.h"
+
+namespace arthip {
+
+// Largest channel counts the register-resident Winograd kernel is built for.
+int winograd_max_kc();  // input channels <= 32 * winograd_max_kc()
+int winograd_max_m();   // output channels
+
+hipError_t launch_winograd(WinoArgs a, hipStream_t s);
+hipError_t launch_direct(DirectArgs a, hipStream_t s);
+
+}  // namespace arthip

@@ -1,0 +1,38 @@
+// Compile-time weight transforms for the conv kernels.
+//
+// Winograd: U = G g G^T per (output, input) channel pair, done once when a
+// plan is built (the reference does the same on the host:
+// src/vapoursynth/hip_engine.cc:972-1018, src/onnxruntime-hip/hip_graph.cc:923-989).
+// The packed layout is this build's own: MFMA A-operand order for
+// v_mfma_f32_16x16x32_f16, scaled by 4 to match the kernel's V/4 transform.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace arthip {
+
+struct WinoGeom {
+  int kc, n_ob, tb, threads;
+  size_t lds;
+};
+
+// Launch geometry / packed sizes (defined in kernels.hip).
+WinoGeom winograd_geom(int C, int M);
+int direct_g8(int M);
+
+// Halfs in the packed U' buffer: [n_ob][16 positions][kc][64 lanes][8].
+size_t winograd_packed_halfs(int C, int M);
+// w is OIHW [M][C][3][3] fp32 (exact fp16 values from the model).
+void winograd_pack(const float* w, int M, int C, uint16_t* out);
+
+// Halfs in the packed direct-conv taps: [g8][8 channels][5 pairs][2].
+size_t direct_packed_halfs(int M);
+// w is OIHW [M][1][3][3] fp32.
+void direct_pack(const float* w, int M, uint16_t* out);
+
+// Bias padded with zeros to the kernels' channel granularity (16), fp32.
+size_t bias_padded_len(int M);
+void bias_pad(const float* bias, int M, float* out);
+
+}  // namespace arthip

@@ -1,0 +1,146 @@
+/*
+ * arthip.h - C ABI of libarthip.so, the MI355X (gfx950) engine for
+ * ArtCNN-style conv-chain upscalers (3x3 convs, ReLU/SiLU, residual adds,
+ * DepthToSpace, Clip) stored as fp16 ONNX models.
+ *
+ * Plain C types only: pointers, sizes, error buffers. Return codes follow the
+ * reference's test driver (tests/correctness/harness/engine_harness.cc:12-15):
+ *   0 = ok, 1 = build / shape / argument failure, 2 = run failure.
+ * Error text is copied NUL-terminated into (err, errlen) when given.
+ */
+#ifndef ARTHIP_H_
+#define ARTHIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ARTHIP_OK 0
+#define ARTHIP_ERR_BUILD 1
+#define ARTHIP_ERR_RUN 2
+
+/* ------------------------------------------------------------------------ */
+/* Engine handle                                                             */
+/*                                                                           */
+/* One engine = one compiled model on one device with its own HIP stream and */
+/* mutex. It replaces vship::HipEngine (src/vapoursynth/hip_engine.h:88-188)  */
+/* and onnxruntime::hip::HipGraph (src/onnxruntime-hip/hip_graph.h:113-167), */
+/* which the VapourSynth plugin and the ONNX Runtime EP each drive.          */
+/* ------------------------------------------------------------------------ */
+
+typedef struct arthip_engine arthip_engine;
+
+/* Creates an engine bound to device_id (HipEngine::HipEngine,
+ * hip_engine.h:90). Fails (1) when the device cannot be selected. */
+int arthip_engine_create(int device_id, arthip_engine** out, char* err, int errlen);
+
+void arthip_engine_destroy(arthip_engine* eng);
+
+/* Parses, validates and fuses an ONNX model (HipEngine::Build,
+ * hip_engine.h:92; hip_engine.cc:197-666). */
+int arthip_engine_build_file(arthip_engine* eng, const char* path, char* err, int errlen);
+int arthip_engine_build_bytes(arthip_engine* eng, const void* data, size_t size, char* err,
+                              int errlen);
+
+/* NCHW output shape for an NCHW input shape (HipEngine::GetOutputShape,
+ * hip_engine.h:95-96). Returns 1 when shape propagation fails. */
+int arthip_engine_output_shape(const arthip_engine* eng, const int64_t in_nchw[4],
+                               int64_t out_nchw[4]);
+
+/* Model IO description (InputIsFp32 / OutputIsFp32 / InputChannels /
+ * OutputChannels, hip_engine.h:116-136). Any pointer may be NULL. */
+int arthip_engine_io_info(const arthip_engine* eng, int* in_fp32, int* out_fp32,
+                          int* in_channels, int* out_channels);
+
+/* One frame from host memory to host memory (HipEngine::Run,
+ * hip_engine.h:102-103): in_host is NCHW in the model's input dtype (fp16, or
+ * fp32 when in_fp32), out_host receives NCHW in the output dtype; out_cap is
+ * its size in bytes. Plans are cached per input shape. */
+int arthip_engine_run(arthip_engine* eng, const void* in_host, const int64_t in_nchw[4],
+                      void* out_host, size_t out_cap, char* err, int errlen);
+
+/* The same with device-resident IO on a caller stream (NULL = the engine's
+ * stream). No host copies and no synchronisation: the caller orders work on
+ * the stream. The reference has no counterpart (its Run always stages through
+ * host memory); this is the entry point for callers whose frames already live
+ * in HBM. */
+int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64_t in_nchw[4],
+                             void* out_dev, void* stream, char* err, int errlen);
+
+/* Human-readable plan of the last built shape (op list, fusions, buffers). */
+int arthip_engine_describe(const arthip_engine* eng, char* buf, int buflen);
+
+/* ------------------------------------------------------------------------ */
+/* Test-driver ABI: same names, arguments and return codes as the reference's */
+/* ctypes driver (tests/correctness/harness/engine_harness.cc:56-210). Each   */
+/* call builds a fresh engine from a model file.                              */
+/* ------------------------------------------------------------------------ */
+
+int engine_device_count(int* count);
+
+int engine_probe(const char* model_path, int N, int H, int W, int C, int device, char* err,
+                 int errlen, int* in_fp32, int* out_fp32, int* cin, int* cout,
+                 int64_t* out_shape, int* out_rank);
+
+int engine_run(const char* model_path, int N, int H, int W, int C, int device,
+               const void* input, size_t input_bytes, void* out, size_t cap,
+               size_t* out_bytes, int* out_fp32, int64_t* out_shape, int* out_rank, char* err,
+               int errlen);
+
+int engine_alloc_failure_then_run(const char* model_path, int N, int bigH, int bigW, int C,
+                                  int device, const void* recovery_input,
+                                  size_t recovery_input_bytes, void* out, size_t cap,
+                                  size_t* out_bytes, int* out_fp32, int64_t* out_shape,
+                                  int* out_rank, char* failerr, int failerrlen, char* runerr,
+                                  int runerrlen);
+
+/* ------------------------------------------------------------------------ */
+/* Kernel-level entry points (one fused conv on device buffers)              */
+/* ------------------------------------------------------------------------ */
+
+/* Sizes of the packed filter buffer (in fp16 elements) and of the padded
+ * fp32 bias buffer for a 3x3 conv with C inputs and M outputs. */
+size_t arthip_conv3x3_packed_halfs(int M, int C);
+size_t arthip_conv3x3_bias_len(int M);
+
+/* Host-side filter transform, done once per layer: the Winograd
+ * U = G g G^T for C > 1 (hip_engine.cc:972-1018), a tap relayout for C == 1
+ * (hip_engine.cc:925-971). w_oihw holds fp16 bits [M][C][3][3]; bias holds M
+ * fp16 values or is NULL. Outputs go to host buffers of the sizes above. */
+int arthip_conv3x3_pack(const uint16_t* w_oihw, const uint16_t* bias, int M, int C,
+                        uint16_t* packed, size_t packed_cap, float* bias_out, size_t bias_cap);
+
+/* out = clip(skip1 + skip0 + act(conv3x3(in) + bias)) on NHWC fp16 device
+ * buffers [N][H][W][C] -> [N][H][W][M]; SAME padding, stride 1. act: 0 none,
+ * 1 ReLU, 2 SiLU. skip0/skip1: NHWC [N][H][W][M] or NULL. The fused form of
+ * the reference's winograd_conv / direct_conv launches
+ * (src/common/hip_kernels.h:143-483). stream may be NULL. */
+int arthip_conv3x3_f16_nhwc(const void* in, const void* packed, const float* bias, int act,
+                            const void* skip0, const void* skip1, void* out, int N, int H, int W,
+                            int C, int M, void* stream);
+
+/* Largest (C, M) the conv kernels accept. */
+int arthip_conv3x3_limits(int* max_c, int* max_m);
+
+/* ------------------------------------------------------------------------ */
+/* Helpers                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* IEEE binary16 round-to-nearest-even conversions
+ * (HipEngine::FloatToHalfBitsRNE / HalfBitsToFloat, hip_engine.h:108-109). */
+uint16_t arthip_f32_to_f16(float f);
+float arthip_f16_to_f32(uint16_t h);
+
+/* Thread-local text of the last failure of a kernel-level call. */
+const char* arthip_last_error(void);
+
+const char* arthip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARTHIP_H_ */

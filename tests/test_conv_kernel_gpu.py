@@ -1,0 +1,150 @@
+"""Kernel-level parity: one fused 3x3 conv through the C ABI vs the CPU oracle.
+
+Covers the Winograd path (C > 1) and the direct head-conv path (C == 1) across
+the reference's geometry sweep (tests/correctness/test_engine.py:18-31) and
+the channel counts of the benchmark configs, with each epilogue option.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from arthip_amd import _lib
+from oracle import ops as orc
+
+pytestmark = pytest.mark.gpu
+
+GEOMETRY = [(8, 8), (8, 17), (8, 24), (8, 25), (17, 16), (17, 17), (33, 17), (16, 33),
+            (33, 33), (64, 64), (1082, 64), (54, 1920)]
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _u16p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+def _f32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def pack(w16: np.ndarray, b16: np.ndarray | None):
+    lib = _lib.lib()
+    m, c = w16.shape[:2]
+    n_u = lib.arthip_conv3x3_packed_halfs(m, c)
+    n_b = lib.arthip_conv3x3_bias_len(m)
+    u = np.zeros(n_u, np.uint16)
+    b = np.zeros(n_b, np.float32)
+    wb = np.ascontiguousarray(w16.view(np.uint16))
+    bb = None if b16 is None else np.ascontiguousarray(b16.view(np.uint16))
+    rc = lib.arthip_conv3x3_pack(_u16p(wb), None if bb is None else _u16p(bb), m, c,
+                                 _u16p(u), n_u, _f32p(b), n_b)
+    assert rc == 0, _lib.last_error()
+    return u, b
+
+
+def run_conv(x16_nchw, w16, b16, act=0, skips=()):
+    """Runs the HIP conv on NCHW fp16 numpy input; returns NCHW fp32."""
+    torch = _torch()
+    lib = _lib.lib()
+    n, c, h, w = x16_nchw.shape
+    m = w16.shape[0]
+    u, b = pack(w16, b16)
+    dev = torch.device("cuda")
+    xin = torch.from_numpy(np.ascontiguousarray(x16_nchw.transpose(0, 2, 3, 1))).to(dev)
+    ut = torch.from_numpy(u.view(np.float16)).to(dev)
+    bt = torch.from_numpy(b).to(dev)
+    sk = [torch.from_numpy(np.ascontiguousarray(s.transpose(0, 2, 3, 1))).to(dev) for s in skips]
+    out = torch.empty((n, h, w, m), dtype=torch.float16, device=dev)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = lib.arthip_conv3x3_f16_nhwc(ptr(xin), ptr(ut), ptr(bt), act,
+                                     ptr(sk[0]) if len(sk) > 0 else None,
+                                     ptr(sk[1]) if len(sk) > 1 else None,
+                                     ptr(out), n, h, w, c, m, None)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    return out.cpu().numpy().astype(np.float32).transpose(0, 3, 1, 2)
+
+
+def oracle_conv(x16, w16, b16, act=0, skips=()):
+    y = orc.conv3x3(x16.astype(np.float32), w16.astype(np.float32),
+                    None if b16 is None else b16.astype(np.float32), acc64=True)
+    if act == 1:
+        y = orc.relu(y)
+    elif act == 2:
+        y = orc.silu(y)
+    for s in skips:
+        y = orc.add(y, s.astype(np.float32))
+    return y
+
+
+def make_case(seed, n, c, m, h, w, scale=1.0):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((n, c, h, w)) * scale).astype(np.float16)
+    wt = (rng.standard_normal((m, c, 3, 3)) * np.sqrt(2.0 / (9 * c))).astype(np.float16)
+    b = rng.uniform(-0.1, 0.1, m).astype(np.float16)
+    return x, wt, b
+
+
+def check(got, ref, label):
+    assert np.isfinite(got).all(), f"{label}: non-finite output"
+    err = np.abs(got - ref)
+    # Error model: the fp16 output rounding costs up to 2^-11 |ref| per element;
+    # fp16 U and V (F(2x2,3x3) Winograd) add roundings of the per-position partial
+    # products, which scale with the typical term size, not with each output.
+    # A wrong index or a dropped term produces errors of the order of rms(ref).
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2))) + 1e-30
+    tol = 2.0 ** -10 * np.abs(ref) + 4e-3 * rms
+    bad = err > tol
+    rel_rms = float(np.sqrt(np.mean((got - ref).astype(np.float64) ** 2))) / rms
+    assert not bad.any(), (f"{label}: {bad.sum()} elements off, max err {err.max():.4g} "
+                           f"at ref {ref.flat[err.argmax()]:.4g} (rms {rms:.3g})")
+    assert rel_rms < 1e-3, f"{label}: relative RMS error {rel_rms:.3g}"
+    return float(err.max())
+
+
+@pytest.mark.parametrize("h,w", GEOMETRY)
+def test_winograd_geometry(h, w):
+    x, wt, b = make_case(1, 1, 4, 4, h, w)
+    check(run_conv(x, wt, b), oracle_conv(x, wt, b), f"c4m4 {h}x{w}")
+
+
+@pytest.mark.parametrize("h,w", GEOMETRY)
+def test_direct_geometry(h, w):
+    x, wt, b = make_case(2, 1, 1, 8, h, w)
+    check(run_conv(x, wt, b), oracle_conv(x, wt, b), f"c1m8 {h}x{w}")
+
+
+@pytest.mark.parametrize("c,m", [(4, 8), (4, 64), (32, 32), (64, 64), (64, 4), (96, 96),
+                                 (4, 128), (3, 5), (48, 24), (1, 64), (1, 4), (1, 96)])
+def test_channel_counts(c, m):
+    x, wt, b = make_case(3, 1, c, m, 37, 45)
+    check(run_conv(x, wt, b), oracle_conv(x, wt, b), f"c{c}m{m}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("nskip", [0, 1, 2])
+def test_epilogue(act, nskip):
+    x, wt, b = make_case(4, 1, 64, 64, 18, 34)
+    rng = np.random.default_rng(5)
+    skips = [rng.standard_normal((1, 64, 18, 34)).astype(np.float16) for _ in range(nskip)]
+    check(run_conv(x, wt, b, act, skips), oracle_conv(x, wt, b, act, skips),
+          f"act{act} skip{nskip}")
+
+
+def test_batch():
+    x, wt, b = make_case(6, 3, 64, 64, 20, 30)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), "batch3")
+
+
+def test_deterministic():
+    x, wt, b = make_case(7, 1, 64, 64, 96, 160)
+    a = run_conv(x, wt, b, 1)
+    for _ in range(3):
+        np.testing.assert_array_equal(a, run_conv(x, wt, b, 1))
