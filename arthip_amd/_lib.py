@@ -47,6 +47,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_engine_run", c_int, eng, c_void, i64p, c_void, c_size, c_char, c_int)
     sig("arthip_engine_run_device", c_int, eng, c_void, i64p, c_void, c_void, c_char, c_int)
     sig("arthip_engine_describe", c_int, eng, c_char, c_int)
+    sig("arthip_engine_set_profiling", c_int, eng, c_int)
+    sig("arthip_engine_profile_read", c_int, eng, c_int, ctypes.POINTER(ctypes.c_double), i64p,
+        c_char, c_int, c_char, c_int)
 
     sig("engine_device_count", c_int, i32p)
     sig("engine_probe", c_int, c_char, c_int, c_int, c_int, c_int, c_int, c_char, c_int,
@@ -62,6 +65,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_conv3x3_f16_nhwc", c_int, c_void, c_void, c_void, c_int, c_void, c_void, c_void,
         c_int, c_int, c_int, c_int, c_int, c_void)
     sig("arthip_conv3x3_limits", c_int, i32p, i32p)
+    sig("arthip_padded_dims", c_int, c_int, c_int, i32p, i32p)
     sig("arthip_f32_to_f16", ctypes.c_uint16, ctypes.c_float)
     sig("arthip_f16_to_f32", ctypes.c_float, ctypes.c_uint16)
     sig("arthip_last_error", c_char)
@@ -73,9 +77,10 @@ EXPORTED_SYMBOLS = (
     "arthip_engine_create", "arthip_engine_destroy", "arthip_engine_build_file",
     "arthip_engine_build_bytes", "arthip_engine_output_shape", "arthip_engine_io_info",
     "arthip_engine_run", "arthip_engine_run_device", "arthip_engine_describe",
+    "arthip_engine_set_profiling", "arthip_engine_profile_read",
     "engine_device_count", "engine_probe", "engine_run", "engine_alloc_failure_then_run",
     "arthip_conv3x3_packed_halfs", "arthip_conv3x3_bias_len", "arthip_conv3x3_pack",
-    "arthip_conv3x3_f16_nhwc", "arthip_conv3x3_limits", "arthip_f32_to_f16",
+    "arthip_conv3x3_f16_nhwc", "arthip_conv3x3_limits", "arthip_padded_dims", "arthip_f32_to_f16",
     "arthip_f16_to_f32", "arthip_last_error", "arthip_version",
 )
 

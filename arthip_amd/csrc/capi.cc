@@ -1,13 +1,20 @@
-// extern "C" kernel-level entry points and helpers (include/arthip.h).
+// extern "C" surface of libarthip.so (include/arthip.h).
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
 #include "arthip.h"
+#include "engine.h"
 #include "half.h"
 #include "launch.h"
 #include "pack.h"
+
+struct arthip_engine {
+  std::unique_ptr<arthip::Engine> eng;
+};
 
 namespace {
 
@@ -18,9 +25,255 @@ int fail(const std::string& msg, int code) {
   return code;
 }
 
+void copy_out(const std::string& s, char* dst, int len) {
+  if (dst == nullptr || len <= 0) return;
+  size_t n = s.size();
+  if (n > static_cast<size_t>(len) - 1) n = static_cast<size_t>(len) - 1;
+  std::memcpy(dst, s.data(), n);
+  dst[n] = '\0';
+}
+
+int report(const std::string& msg, int code, char* err, int errlen) {
+  t_last_error = msg;
+  copy_out(msg, err, errlen);
+  return code;
+}
+
+constexpr int kMaxRank = 8;
+
+void write_shape(const int64_t s[4], int64_t* out_shape, int* out_rank) {
+  if (out_rank) *out_rank = 4;
+  if (out_shape)
+    for (int i = 0; i < 4 && i < kMaxRank; ++i) out_shape[i] = s[i];
+}
+
+// Fresh engine built from a model file (the test driver builds one per call,
+// tests/correctness/harness/engine_harness.cc:63-145).
+int make_engine(const char* path, int device, std::unique_ptr<arthip::Engine>& out,
+                std::string& error) {
+  if (path == nullptr) {
+    error = "failed to parse model file (null path)";
+    return ARTHIP_ERR_BUILD;
+  }
+  auto e = std::make_unique<arthip::Engine>(device);
+  if (!e->BuildFile(path, error)) return ARTHIP_ERR_BUILD;
+  if (!e->Init(error)) return ARTHIP_ERR_BUILD;
+  out = std::move(e);
+  return ARTHIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+// ---------------------------------------------------------------------------
+// Engine handle
+// ---------------------------------------------------------------------------
+
+int arthip_engine_create(int device_id, arthip_engine** out, char* err, int errlen) {
+  if (out == nullptr) return report("null output handle", ARTHIP_ERR_BUILD, err, errlen);
+  *out = nullptr;
+  auto h = std::make_unique<arthip_engine>();
+  h->eng = std::make_unique<arthip::Engine>(device_id);
+  *out = h.release();
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+void arthip_engine_destroy(arthip_engine* eng) { delete eng; }
+
+int arthip_engine_build_file(arthip_engine* eng, const char* path, char* err, int errlen) {
+  if (eng == nullptr || path == nullptr)
+    return report("null engine or path", ARTHIP_ERR_BUILD, err, errlen);
+  std::string e;
+  if (!eng->eng->BuildFile(path, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_build_bytes(arthip_engine* eng, const void* data, size_t size, char* err,
+                              int errlen) {
+  if (eng == nullptr || data == nullptr)
+    return report("null engine or model bytes", ARTHIP_ERR_BUILD, err, errlen);
+  std::string e;
+  if (!eng->eng->Build(data, size, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_output_shape(const arthip_engine* eng, const int64_t in_nchw[4],
+                               int64_t out_nchw[4]) {
+  if (eng == nullptr || in_nchw == nullptr || out_nchw == nullptr)
+    return fail("null argument", ARTHIP_ERR_BUILD);
+  if (!eng->eng->OutputShape(in_nchw, out_nchw)) return fail("shape propagation failed", ARTHIP_ERR_BUILD);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_io_info(const arthip_engine* eng, int* in_fp32, int* out_fp32, int* in_channels,
+                          int* out_channels) {
+  if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);
+  if (in_fp32) *in_fp32 = eng->eng->InputFp32() ? 1 : 0;
+  if (out_fp32) *out_fp32 = eng->eng->OutputFp32() ? 1 : 0;
+  if (in_channels) *in_channels = eng->eng->InputChannels();
+  if (out_channels) *out_channels = eng->eng->OutputChannels();
+  return ARTHIP_OK;
+}
+
+int arthip_engine_run(arthip_engine* eng, const void* in_host, const int64_t in_nchw[4],
+                      void* out_host, size_t out_cap, char* err, int errlen) {
+  if (eng == nullptr || in_nchw == nullptr)
+    return report("null engine or shape", ARTHIP_ERR_BUILD, err, errlen);
+  int64_t o[4];
+  if (!eng->eng->OutputShape(in_nchw, o))
+    return report("shape propagation failed", ARTHIP_ERR_BUILD, err, errlen);
+  std::string e;
+  if (!eng->eng->Run(in_host, in_nchw, out_host, out_cap, e))
+    return report(e, ARTHIP_ERR_RUN, err, errlen);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64_t in_nchw[4],
+                             void* out_dev, void* stream, char* err, int errlen) {
+  if (eng == nullptr || in_nchw == nullptr)
+    return report("null engine or shape", ARTHIP_ERR_BUILD, err, errlen);
+  int64_t o[4];
+  if (!eng->eng->OutputShape(in_nchw, o))
+    return report("shape propagation failed", ARTHIP_ERR_BUILD, err, errlen);
+  std::string e;
+  if (!eng->eng->RunDevice(in_dev, in_nchw, out_dev, static_cast<hipStream_t>(stream), e))
+    return report(e, ARTHIP_ERR_RUN, err, errlen);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_describe(const arthip_engine* eng, char* buf, int buflen) {
+  if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);
+  copy_out(eng->eng->Describe(), buf, buflen);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_set_profiling(arthip_engine* eng, int on) {
+  if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);
+  eng->eng->SetProfiling(on != 0);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_ms,
+                               int64_t* launches, char* names, int names_len, char* err,
+                               int errlen) {
+  if (eng == nullptr) return -report("null engine", ARTHIP_ERR_BUILD, err, errlen);
+  std::vector<arthip::Engine::StepProfile> prof;
+  std::string e;
+  if (!eng->eng->ProfileRead(prof, e)) return -report(e, ARTHIP_ERR_RUN, err, errlen);
+  std::string joined;
+  const int n = static_cast<int>(prof.size());
+  for (int i = 0; i < n; ++i) {
+    if (i < max_steps) {
+      if (total_ms) total_ms[i] = prof[i].total_ms;
+      if (launches) launches[i] = prof[i].launches;
+    }
+    joined += prof[i].name;
+    joined += '\n';
+  }
+  copy_out(joined, names, names_len);
+  copy_out("", err, errlen);
+  return n;
+}
+
+// ---------------------------------------------------------------------------
+// Test-driver ABI (engine_harness.cc:56-210)
+// ---------------------------------------------------------------------------
+
+int engine_device_count(int* count) {
+  if (count == nullptr) return ARTHIP_ERR_BUILD;
+  if (hipInit(0) != hipSuccess) return ARTHIP_ERR_BUILD;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return ARTHIP_ERR_BUILD;
+  *count = n;
+  return ARTHIP_OK;
+}
+
+int engine_probe(const char* model_path, int N, int H, int W, int C, int device, char* err,
+                 int errlen, int* in_fp32, int* out_fp32, int* cin, int* cout,
+                 int64_t* out_shape, int* out_rank) {
+  std::unique_ptr<arthip::Engine> eng;
+  std::string e;
+  if (make_engine(model_path, device, eng, e) != ARTHIP_OK) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  if (in_fp32) *in_fp32 = eng->InputFp32() ? 1 : 0;
+  if (out_fp32) *out_fp32 = eng->OutputFp32() ? 1 : 0;
+  if (cin) *cin = eng->InputChannels();
+  if (cout) *cout = eng->OutputChannels();
+  const int64_t in[4] = {N, C, H, W};
+  int64_t o[4];
+  if (!eng->OutputShape(in, o)) return report("shape propagation failed", ARTHIP_ERR_BUILD, err, errlen);
+  write_shape(o, out_shape, out_rank);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int engine_run(const char* model_path, int N, int H, int W, int C, int device,
+               const void* input, size_t input_bytes, void* out, size_t cap,
+               size_t* out_bytes, int* out_fp32, int64_t* out_shape, int* out_rank, char* err,
+               int errlen) {
+  std::unique_ptr<arthip::Engine> eng;
+  std::string e;
+  if (make_engine(model_path, device, eng, e) != ARTHIP_OK) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  const int64_t in[4] = {N, C, H, W};
+  int64_t o[4];
+  if (!eng->OutputShape(in, o)) return report("shape propagation failed", ARTHIP_ERR_BUILD, err, errlen);
+  const size_t need = eng->OutputBytes(in);
+  if (need > cap) return report("output buffer too small", ARTHIP_ERR_BUILD, err, errlen);
+  const size_t expect = eng->InputBytes(in);
+  if (input == nullptr || input_bytes != expect)
+    return report("input buffer size mismatch (expected " + std::to_string(expect) +
+                      " bytes, got " + std::to_string(input_bytes) + ")",
+                  ARTHIP_ERR_BUILD, err, errlen);
+  if (!eng->Run(input, in, out, cap, e)) return report(e, ARTHIP_ERR_RUN, err, errlen);
+  if (out_bytes) *out_bytes = need;
+  if (out_fp32) *out_fp32 = eng->OutputFp32() ? 1 : 0;
+  write_shape(o, out_shape, out_rank);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int engine_alloc_failure_then_run(const char* model_path, int N, int bigH, int bigW, int C,
+                                  int device, const void* recovery_input,
+                                  size_t recovery_input_bytes, void* out, size_t cap,
+                                  size_t* out_bytes, int* out_fp32, int64_t* out_shape,
+                                  int* out_rank, char* failerr, int failerrlen, char* runerr,
+                                  int runerrlen) {
+  std::unique_ptr<arthip::Engine> eng;
+  std::string e;
+  if (make_engine(model_path, device, eng, e) != ARTHIP_OK)
+    return report("build failed: " + e, ARTHIP_ERR_BUILD, failerr, failerrlen);
+  char dummy[8] = {0};
+  const int64_t big[4] = {N, C, bigH, bigW};
+  std::string first;
+  if (eng->Run(dummy, big, dummy, sizeof(dummy), first))
+    return report("expected the oversized run to fail but it succeeded", ARTHIP_ERR_BUILD, failerr,
+                  failerrlen);
+  copy_out(first, failerr, failerrlen);
+  const int64_t in[4] = {N, C, 16, 16};
+  int64_t o[4];
+  if (!eng->OutputShape(in, o)) return report("recovery shape probe failed", ARTHIP_ERR_RUN, runerr, runerrlen);
+  const size_t need = eng->OutputBytes(in);
+  if (need > cap) return report("recovery output buffer too small", ARTHIP_ERR_RUN, runerr, runerrlen);
+  if (recovery_input == nullptr || recovery_input_bytes != eng->InputBytes(in))
+    return report("recovery input buffer size mismatch", ARTHIP_ERR_RUN, runerr, runerrlen);
+  std::string second;
+  if (!eng->Run(recovery_input, in, out, cap, second))
+    return report(second, ARTHIP_ERR_RUN, runerr, runerrlen);
+  if (out_bytes) *out_bytes = need;
+  if (out_fp32) *out_fp32 = eng->OutputFp32() ? 1 : 0;
+  write_shape(o, out_shape, out_rank);
+  copy_out("", runerr, runerrlen);
+  return ARTHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel-level entry points
+// ---------------------------------------------------------------------------
 
 uint16_t arthip_f32_to_f16(float f) { return arthip::f32_to_f16(f); }
 float arthip_f16_to_f32(uint16_t h) { return arthip::f16_to_f32(h); }
@@ -30,6 +283,13 @@ const char* arthip_version(void) { return "arthip-mi355x 0.1.0 (gfx950)"; }
 int arthip_conv3x3_limits(int* max_c, int* max_m) {
   if (max_c) *max_c = 32 * arthip::winograd_max_kc();
   if (max_m) *max_m = arthip::winograd_max_m();
+  return ARTHIP_OK;
+}
+
+int arthip_padded_dims(int H, int W, int* Hp, int* Wp) {
+  if (H < 1 || W < 1) return fail("arthip_padded_dims: non-positive size", ARTHIP_ERR_BUILD);
+  if (Hp) *Hp = static_cast<int>(arthip::padded_rows(H));
+  if (Wp) *Wp = static_cast<int>(arthip::padded_cols(W));
   return ARTHIP_OK;
 }
 
@@ -44,6 +304,8 @@ int arthip_conv3x3_pack(const uint16_t* w_oihw, const uint16_t* bias, int M, int
                         uint16_t* packed, size_t packed_cap, float* bias_out, size_t bias_cap) {
   if (w_oihw == nullptr || packed == nullptr || bias_out == nullptr || M <= 0 || C <= 0)
     return fail("arthip_conv3x3_pack: null buffer or non-positive channel count", ARTHIP_ERR_BUILD);
+  if (C > 32 * arthip::winograd_max_kc() || M > arthip::winograd_max_m())
+    return fail("arthip_conv3x3_pack: channel count beyond kernel limits", ARTHIP_ERR_BUILD);
   if (packed_cap < arthip_conv3x3_packed_halfs(M, C) || bias_cap < arthip_conv3x3_bias_len(M))
     return fail("arthip_conv3x3_pack: output buffer too small", ARTHIP_ERR_BUILD);
   std::vector<float> w(static_cast<size_t>(M) * C * 9);
@@ -75,7 +337,7 @@ int arthip_conv3x3_f16_nhwc(const void* in, const void* packed, const float* bia
   e.skip1 = static_cast<const uint16_t*>(skip1);
   e.out = out;
   e.act = act;
-  e.out_kind = arthip::kOutNhwcF16;
+  e.out_kind = arthip::kOutPadded;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err;
   if (C == 1) {

@@ -1,10 +1,17 @@
 // Launch arguments shared by the host launchers and the gfx950 kernels.
 //
-// Activations inside the engine are NHWC fp16 ([n][h][w][c], channels
-// contiguous). The final op of a graph may instead write the public NCHW
-// boundary layout directly, in fp16 or fp32, optionally through a fused
-// DepthToSpace (DCR) and Clip.
+// Internal activations are "padded NHWC" fp16: [n][Hp][Wp][c] with a zero
+// border, Hp = 2*ceil(H/2) + 2 and Wp = 2*ceil(W/2) + 2, pixel (h, w) stored
+// at row h+1, column w+1. Every 4x4 Winograd input patch and every 3x3 direct
+// window then lies inside the buffer, so the conv kernels load without bounds
+// checks. The border is zeroed once when a buffer is allocated and is never
+// written afterwards.
+//
+// The graph boundary (engine input and output) is plain NCHW in fp16 or fp32,
+// like the reference's host interface (src/vapoursynth/hip_engine.h:98-103).
 #pragma once
+
+#include <hip/hip_runtime.h>
 
 #include <cstdint>
 
@@ -13,33 +20,40 @@ namespace arthip {
 enum Act : int32_t { kActNone = 0, kActRelu = 1, kActSilu = 2 };
 
 enum OutKind : int32_t {
-  kOutNhwcF16 = 0,  // internal activation layout
+  kOutPadded = 0,   // internal padded NHWC fp16
   kOutNchwF16 = 1,  // boundary layout, fp16
   kOutNchwF32 = 2,  // boundary layout, fp32 (a folded output Cast)
 };
 
-// Epilogue applied to every conv output element, in this order, all in fp32:
-//   y = acc + bias[m]; y = act(y); y += skip0; y += skip1; y = clip(y);
-// then one rounding to the output dtype. A fused DepthToSpace permutes the
-// destination index only.
+__host__ __device__ inline int64_t padded_rows(int64_t h) { return 2 * ((h + 1) / 2) + 2; }
+__host__ __device__ inline int64_t padded_cols(int64_t w) { return 2 * ((w + 1) / 2) + 2; }
+
+// Epilogue applied to every conv output element:
+//   y = acc + bias[m]; y = act(y); y += skip0; y += skip1; y = clip(y)
+// The fast path (padded NHWC output, M % 4 == 0, no clip) rounds acc + bias to
+// fp16 once and applies act and the residual adds in fp16 arithmetic (each add
+// rounds once, like the fp16 tensors between ONNX nodes); the general path keeps
+// fp32 until one final rounding. A fused DepthToSpace permutes the destination
+// index of a boundary-layout output.
 struct Epilogue {
-  const float* bias;       // [m_pad] fp32, zero padded (never null)
-  const uint16_t* skip0;   // NHWC fp16 [n][h][w][M], or null
-  const uint16_t* skip1;   // NHWC fp16 [n][h][w][M], or null
+  const float* bias;      // [m_pad] fp32, zero padded (never null)
+  const uint16_t* skip0;  // padded NHWC fp16 with the output's geometry, or null
+  const uint16_t* skip1;
   void* out;
-  int32_t act;             // Act
-  int32_t out_kind;        // OutKind
-  int32_t dts_b;           // >= 2: fused DepthToSpace(DCR) with this block size; else 0
+  int32_t act;       // Act
+  int32_t out_kind;  // OutKind
+  int32_t dts_b;     // >= 2: fused DepthToSpace(DCR) (boundary output only); else 0
   int32_t do_clip;
   float clip_lo, clip_hi;
 };
 
-// Winograd F(2x2,3x3) conv, C > 1 (see winograd_conv in kernels.hip).
+// Winograd F(2x2,3x3) conv, C > 1 (winograd_conv in kernels.hip).
 struct WinoArgs {
-  const uint16_t* in;  // NHWC fp16 [N][H][W][C]
+  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C]
   const uint16_t* u;   // packed transformed filters (winograd_pack)
   Epilogue epi;
   int32_t N, H, W, C, M;
+  int32_t Hp, Wp;            // padded geometry shared by input, skips and padded output
   int32_t tiles_h, tiles_w;  // ceil(H/2), ceil(W/2)
   int32_t n_ob;              // 16-wide output-channel blocks (= waves per tile block)
   int32_t tb;                // 16-tile column blocks per work item
@@ -49,11 +63,42 @@ struct WinoArgs {
 
 // Direct 3x3 conv for a single input channel (the model's head conv).
 struct DirectArgs {
-  const uint16_t* in;  // NHWC fp16 [N][H][W][1]
+  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][1]
   const uint16_t* w;   // packed taps: [g8][8 ch][5 x half2] (direct_pack)
   Epilogue epi;
   int32_t N, H, W, M;
-  int32_t g8;          // threads per pixel (power of two >= ceil(M/8))
+  int32_t Hp, Wp;
+  int32_t g8;  // threads per pixel (power of two >= ceil(M/8))
+};
+
+// Elementwise / layout kernels for the ops the conv epilogues do not absorb.
+enum UnaryOp : int32_t { kUnarySigmoid = 0, kUnaryRelu = 1, kUnaryClip = 2 };
+enum BinaryOp : int32_t { kBinaryAdd = 0, kBinaryMul = 1 };
+
+struct EltArgs {
+  const uint16_t* a;  // padded NHWC fp16
+  const uint16_t* b;  // second operand (binary) or null
+  uint16_t* out;      // padded NHWC fp16, same geometry
+  int32_t N, H, W, C, Hp, Wp;
+  int32_t op;
+  float lo, hi;
+};
+
+struct DtsArgs {
+  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C]
+  void* out;           // padded NHWC fp16 (kOutPadded) or boundary NCHW
+  int32_t N, H, W, C, Hp, Wp;  // input geometry
+  int32_t b;                   // block size; output channels = C / (b*b)
+  int32_t out_kind;
+  int32_t do_clip;
+  float lo, hi;
+};
+
+struct IoArgs {
+  const void* src;
+  void* dst;
+  int32_t N, H, W, C, Hp, Wp;
+  int32_t fp32;  // boundary side is fp32
 };
 
 }  // namespace arthip

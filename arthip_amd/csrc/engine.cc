@@ -1,0 +1,664 @@
+#include "engine.h"
+
+#include <algorithm>
+#include <cstring>
+#include <sstream>
+
+#include "half.h"
+#include "launch.h"
+#include "pack.h"
+
+namespace arthip {
+
+namespace {
+
+std::string HipErr(const char* what, hipError_t e) {
+  return std::string(what) + " failed: " + hipGetErrorString(e);
+}
+
+size_t PaddedBytes(const Shape& s) {
+  return static_cast<size_t>(s.n) * static_cast<size_t>(padded_rows(s.h)) *
+         static_cast<size_t>(padded_cols(s.w)) * static_cast<size_t>(s.c) * 2;
+}
+
+}  // namespace
+
+Engine::Engine(int device_id) : device_(device_id) {}
+
+Engine::~Engine() {
+  FreeAll();
+  for (const EventPair& ev : pending_events_) {
+    hipEventDestroy(ev.start);
+    hipEventDestroy(ev.stop);
+  }
+  for (hipEvent_t e : event_pool_) hipEventDestroy(e);
+  if (stream_) {
+    hipSetDevice(device_);
+    hipStreamDestroy(stream_);
+  }
+}
+
+bool Engine::SetDevice(std::string& error) const {
+  const hipError_t e = hipSetDevice(device_);
+  if (e != hipSuccess) {
+    error = "hipSetDevice(" + std::to_string(device_) + ") failed: " + hipGetErrorString(e);
+    return false;
+  }
+  return true;
+}
+
+bool Engine::Init(std::string& error) {
+  if (stream_ != nullptr) return SetDevice(error);
+  const hipError_t ie = hipInit(0);
+  if (ie != hipSuccess) {
+    error = HipErr("hipInit", ie);
+    return false;
+  }
+  if (!SetDevice(error)) return false;
+  if (stream_ == nullptr) {
+    const hipError_t e = hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      error = HipErr("hipStreamCreate", e);
+      return false;
+    }
+  }
+  return true;
+}
+
+bool Engine::Build(const void* data, size_t size, std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  onnx::Model model;
+  if (!onnx::ParseModel(data, size, model, error)) return false;
+  FreeAll();
+  built_ = false;
+  if (!BuildGraph(model, graph_, error)) return false;
+  built_ = true;
+  return true;
+}
+
+bool Engine::BuildFile(const std::string& path, std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  onnx::Model model;
+  if (!onnx::LoadModelFile(path, model, error)) return false;
+  FreeAll();
+  built_ = false;
+  if (!BuildGraph(model, graph_, error)) return false;
+  built_ = true;
+  return true;
+}
+
+int Engine::InputChannels() const {
+  for (const Op& op : graph_.ops)
+    if (op.kind == OpKind::Conv) return static_cast<int>(graph_.weights.at(op.weight).dims[1]);
+  return 1;
+}
+
+int Engine::OutputChannels() const {
+  for (auto it = graph_.ops.rbegin(); it != graph_.ops.rend(); ++it)
+    if (it->kind == OpKind::Conv) return static_cast<int>(graph_.weights.at(it->weight).dims[0]);
+  return 1;
+}
+
+bool Engine::OutputShape(const int64_t in[4], int64_t out[4]) const {
+  if (!built_) return false;
+  std::unordered_map<std::string, Shape> shapes;
+  if (!PropagateShapes(graph_, in, shapes)) return false;
+  const Shape& s = shapes.at(graph_.output_name);
+  out[0] = s.n;
+  out[1] = s.c;
+  out[2] = s.h;
+  out[3] = s.w;
+  return true;
+}
+
+size_t Engine::InputBytes(const int64_t in[4]) const {
+  return static_cast<size_t>(in[0] * in[1] * in[2] * in[3]) * (graph_.input_fp32 ? 4 : 2);
+}
+
+size_t Engine::OutputBytes(const int64_t in[4]) const {
+  int64_t o[4];
+  if (!OutputShape(in, o)) return 0;
+  return static_cast<size_t>(o[0] * o[1] * o[2] * o[3]) * (graph_.output_fp32 ? 4 : 2);
+}
+
+void Engine::FreePlan() {
+  prof_acc_.clear();
+  const bool any = !bufs_.empty() || in_stage_dev_ || out_stage_dev_ || in_pinned_ || out_pinned_;
+  if (any) hipSetDevice(device_);  // frees need the owning device current on this thread
+  for (auto& b : bufs_)
+    if (b.ptr) hipFree(b.ptr);
+  bufs_.clear();
+  buf_names_.clear();
+  steps_.clear();
+  if (in_stage_dev_) hipFree(in_stage_dev_);
+  if (out_stage_dev_) hipFree(out_stage_dev_);
+  if (in_pinned_) hipHostFree(in_pinned_);
+  if (out_pinned_) hipHostFree(out_pinned_);
+  in_stage_dev_ = out_stage_dev_ = in_pinned_ = out_pinned_ = nullptr;
+  in_bytes_ = out_bytes_ = 0;
+  planned_ = false;
+}
+
+void Engine::FreeAll() {
+  FreePlan();
+  if (!wbufs_.empty()) hipSetDevice(device_);
+  for (auto& b : wbufs_)
+    if (b.ptr) hipFree(b.ptr);
+  wbufs_.clear();
+  op_wbuf_.clear();
+  op_bbuf_.clear();
+  weights_ready_ = false;
+}
+
+// Winograd / direct filter transforms for every conv, done once and kept
+// across plans (weights do not depend on the input shape).
+bool Engine::EnsureWeights(std::string& error) {
+  if (weights_ready_) return true;
+  auto upload = [&](const void* host, size_t bytes, int& idx) -> bool {
+    DevBuf b;
+    hipError_t e = hipMalloc(&b.ptr, bytes);
+    if (e != hipSuccess) {
+      error = "hipMalloc of " + std::to_string(bytes) + " bytes for packed weights failed: " +
+              hipGetErrorString(e);
+      return false;
+    }
+    b.bytes = bytes;
+    wbufs_.push_back(b);
+    idx = static_cast<int>(wbufs_.size()) - 1;
+    e = hipMemcpy(b.ptr, host, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      error = HipErr("hipMemcpy of packed weights", e);
+      return false;
+    }
+    return true;
+  };
+  for (size_t i = 0; i < graph_.ops.size(); ++i) {
+    const Op& op = graph_.ops[i];
+    if (op.kind != OpKind::Conv) continue;
+    const Weight& w = graph_.weights.at(op.weight);
+    const int M = static_cast<int>(w.dims[0]);
+    const int C = static_cast<int>(w.dims[1]);
+    // Weights are rounded to fp16 first: the model's compute precision.
+    std::vector<float> wf(static_cast<size_t>(M) * C * 9);
+    for (size_t k = 0; k < wf.size(); ++k) wf[k] = f16_to_f32(f32_to_f16(WeightAt(w, k)));
+    std::vector<float> bf(static_cast<size_t>(M), 0.0f);
+    if (!op.bias.empty()) {
+      const Weight& b = graph_.weights.at(op.bias);
+      for (int k = 0; k < M; ++k) bf[k] = f16_to_f32(f32_to_f16(WeightAt(b, k)));
+    }
+    std::vector<uint16_t> packed;
+    if (C == 1) {
+      packed.resize(direct_packed_halfs(M));
+      direct_pack(wf.data(), M, packed.data());
+    } else {
+      packed.resize(winograd_packed_halfs(C, M));
+      winograd_pack(wf.data(), M, C, packed.data());
+    }
+    std::vector<float> bias(bias_padded_len(M));
+    bias_pad(bf.data(), M, bias.data());
+    int wi = -1, bi = -1;
+    if (!upload(packed.data(), packed.size() * 2, wi) ||
+        !upload(bias.data(), bias.size() * 4, bi)) {
+      FreeAll();
+      return false;
+    }
+    op_wbuf_[static_cast<int>(i)] = wi;
+    op_bbuf_[static_cast<int>(i)] = bi;
+  }
+  weights_ready_ = true;
+  return true;
+}
+
+bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
+  if (planned_ && std::equal(in, in + 4, plan_in_)) return true;
+  if (!built_) {
+    error = "engine has no model (build first)";
+    return false;
+  }
+  FreePlan();
+  std::unordered_map<std::string, Shape> shapes;
+  if (!PropagateShapes(graph_, in, shapes)) {
+    error = "shape propagation failed (unsupported convolution geometry, channel mismatch, "
+            "residual/binary operand shape mismatch, or DepthToSpace block size)";
+    return false;
+  }
+  if (!EnsureWeights(error)) return false;
+
+  const auto& ops = graph_.ops;
+  const int nops = static_cast<int>(ops.size());
+  // Last op index reading each tensor; the graph output lives to the end.
+  std::unordered_map<std::string, int> last_use;
+  for (int i = 0; i < nops; ++i) {
+    last_use[ops[i].in0] = i;
+    if (!ops[i].in1.empty()) last_use[ops[i].in1] = i;
+    for (const auto& s : ops[i].skips) last_use[s] = i;
+  }
+  last_use[graph_.output_name] = nops;
+
+  // The final op writes the boundary output itself when it can (a conv, with
+  // or without a fused DepthToSpace, or a DepthToSpace) and nothing else
+  // reads that tensor; otherwise an output conversion step follows.
+  int final_op = -1;
+  for (int i = 0; i < nops; ++i)
+    if (ops[i].out == graph_.output_name) final_op = i;
+  bool output_read_inside = false;
+  for (int i = 0; i < nops; ++i) {
+    const Op& o = ops[i];
+    bool r = o.in0 == graph_.output_name || o.in1 == graph_.output_name;
+    for (const auto& s : o.skips) r = r || s == graph_.output_name;
+    output_read_inside = output_read_inside || r;
+  }
+  const bool direct_out = final_op >= 0 && !output_read_inside &&
+                          (ops[final_op].kind == OpKind::Conv ||
+                           ops[final_op].kind == OpKind::DepthToSpace);
+
+  // Liveness-based buffer reuse (hip_engine.cc:819-898): a buffer is recycled
+  // for a tensor of identical padded geometry once every reader of its
+  // previous tensor has run. Matching geometry keeps the zero border intact.
+  struct Slot {
+    int buf;
+    int free_after;  // op index of the last reader of the current tensor
+    Shape geo;
+  };
+  std::vector<Slot> slots;
+  std::unordered_map<std::string, int> tbuf;  // tensor -> buffer index
+  auto alloc = [&](const std::string& name, const Shape& s, int producer) -> bool {
+    for (auto& sl : slots) {
+      if (sl.free_after < producer && sl.geo == s) {
+        sl.free_after = last_use.count(name) ? last_use[name] : producer;
+        tbuf[name] = sl.buf;
+        return true;
+      }
+    }
+    DevBuf b;
+    b.bytes = PaddedBytes(s);
+    const hipError_t e = hipMalloc(&b.ptr, b.bytes);
+    if (e != hipSuccess) {
+      error = "hipMalloc of " + std::to_string(b.bytes) + " bytes for tensor '" + name +
+              "' failed: " + hipGetErrorString(e);
+      return false;
+    }
+    bufs_.push_back(b);
+    buf_names_.push_back(name);
+    const int idx = static_cast<int>(bufs_.size()) - 1;
+    const hipError_t z = hipMemsetAsync(b.ptr, 0, b.bytes, stream_);  // zero border
+    if (z != hipSuccess) {
+      error = HipErr("hipMemsetAsync of an activation buffer", z);
+      return false;
+    }
+    slots.push_back(Slot{idx, last_use.count(name) ? last_use[name] : producer, s});
+    tbuf[name] = idx;
+    return true;
+  };
+
+  auto fail = [&]() {
+    FreePlan();
+    return false;
+  };
+
+  // Boundary input -> internal padded tensor.
+  const Shape sin = shapes.at(graph_.input_name);
+  if (!alloc(graph_.input_name, sin, -1)) return fail();
+  {
+    Step st;
+    st.kind = StepKind::InputConvert;
+    st.in = kBoundaryIn;
+    st.out = tbuf[graph_.input_name];
+    st.N = (int32_t)sin.n; st.H = (int32_t)sin.h; st.W = (int32_t)sin.w; st.C = (int32_t)sin.c;
+    st.fp32 = graph_.input_fp32 ? 1 : 0;
+    steps_.push_back(st);
+  }
+
+  const int out_kind_boundary = graph_.output_fp32 ? kOutNchwF32 : kOutNchwF16;
+  for (int i = 0; i < nops; ++i) {
+    const Op& op = ops[i];
+    const Shape si = shapes.at(op.in0);
+    const Shape so = shapes.at(op.out);
+    const bool to_boundary = direct_out && i == final_op;
+    int out_buf = kBoundaryOut;
+    if (!to_boundary && !alloc(op.out, so, i)) return fail();
+    if (!to_boundary) out_buf = tbuf[op.out];
+
+    Step st;
+    st.op = i;
+    st.in = tbuf.at(op.in0);
+    st.out = out_buf;
+    st.N = (int32_t)si.n; st.H = (int32_t)si.h; st.W = (int32_t)si.w; st.C = (int32_t)si.c;
+    switch (op.kind) {
+      case OpKind::Conv: {
+        const Weight& w = graph_.weights.at(op.weight);
+        st.M = static_cast<int32_t>(w.dims[0]);
+        st.kind = st.C == 1 ? StepKind::ConvDirect : StepKind::ConvWinograd;
+        st.wbuf = op_wbuf_.at(i);
+        st.bbuf = op_bbuf_.at(i);
+        for (size_t k = 0; k < op.skips.size(); ++k) st.skip[k] = tbuf.at(op.skips[k]);
+        st.epi.act = op.act;
+        st.epi.out_kind = to_boundary ? out_kind_boundary : kOutPadded;
+        st.epi.dts_b = (to_boundary && op.dts_b >= 2) ? op.dts_b : 0;
+        st.epi.do_clip = op.clip ? 1 : 0;
+        st.epi.clip_lo = op.clip_lo;
+        st.epi.clip_hi = op.clip_hi;
+        if (op.dts_b >= 1 && !to_boundary) {
+          error = "internal error: fused DepthToSpace conv does not write the graph output";
+          return fail();
+        }
+        break;
+      }
+      case OpKind::Sigmoid:
+      case OpKind::Relu:
+      case OpKind::Clip:
+        st.kind = StepKind::Eltwise;
+        st.elt_op = op.kind == OpKind::Sigmoid ? kUnarySigmoid
+                    : op.kind == OpKind::Relu  ? kUnaryRelu
+                                               : kUnaryClip;
+        st.lo = op.clip_lo;
+        st.hi = op.clip_hi;
+        if (to_boundary) {
+          error = "internal error: elementwise op cannot write the boundary";
+          return fail();
+        }
+        break;
+      case OpKind::Add:
+      case OpKind::Mul:
+        st.kind = StepKind::Eltwise;
+        st.binary = true;
+        st.elt_op = op.kind == OpKind::Mul ? kBinaryMul : kBinaryAdd;
+        st.in2 = tbuf.at(op.in1);
+        break;
+      case OpKind::DepthToSpace:
+        st.kind = StepKind::DepthToSpace;
+        st.dts_b = op.blocksize;
+        st.out_kind = to_boundary ? out_kind_boundary : kOutPadded;
+        st.do_clip = op.clip ? 1 : 0;
+        st.lo = op.clip_lo;
+        st.hi = op.clip_hi;
+        break;
+    }
+    steps_.push_back(st);
+  }
+
+  if (!direct_out) {
+    const Shape so = shapes.at(graph_.output_name);
+    Step st;
+    st.kind = StepKind::OutputConvert;
+    st.in = tbuf.at(graph_.output_name);
+    st.out = kBoundaryOut;
+    st.N = (int32_t)so.n; st.H = (int32_t)so.h; st.W = (int32_t)so.w; st.C = (int32_t)so.c;
+    st.fp32 = graph_.output_fp32 ? 1 : 0;
+    steps_.push_back(st);
+  }
+
+  in_bytes_ = InputBytes(in);
+  out_bytes_ = OutputBytes(in);
+  hipError_t e = hipStreamSynchronize(stream_);  // buffer zeroing done
+  if (e != hipSuccess) {
+    error = HipErr("hipStreamSynchronize after plan setup", e);
+    return fail();
+  }
+  std::copy(in, in + 4, plan_in_);
+  planned_ = true;
+  return true;
+}
+
+bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::string& error) {
+  auto ptr = [&](int idx) -> void* {
+    if (idx == kBoundaryIn) return const_cast<void*>(in_dev);
+    if (idx == kBoundaryOut) return out_dev;
+    if (idx < 0) return nullptr;
+    return bufs_[idx].ptr;
+  };
+  if (profiling_ && prof_acc_.size() != steps_.size()) {
+    prof_acc_.assign(steps_.size(), StepProfile{});
+    for (size_t i = 0; i < steps_.size(); ++i) prof_acc_[i].name = StepName(steps_[i]);
+  }
+  for (size_t i = 0; i < steps_.size(); ++i) {
+    const Step& st = steps_[i];
+    hipError_t e = hipSuccess;
+    EventPair ev{static_cast<int>(i), nullptr, nullptr};
+    if (profiling_) {
+      ev.start = TakeEvent();
+      ev.stop = TakeEvent();
+      if (ev.start == nullptr || ev.stop == nullptr || hipEventRecord(ev.start, s) != hipSuccess) {
+        error = "HIP event creation/record for profiling failed";
+        return false;
+      }
+    }
+    switch (st.kind) {
+      case StepKind::InputConvert:
+      case StepKind::OutputConvert: {
+        IoArgs a{};
+        a.src = ptr(st.in);
+        a.dst = ptr(st.out);
+        a.N = st.N; a.H = st.H; a.W = st.W; a.C = st.C;
+        a.Hp = (int32_t)padded_rows(st.H);
+        a.Wp = (int32_t)padded_cols(st.W);
+        a.fp32 = st.fp32;
+        e = st.kind == StepKind::InputConvert ? launch_input_convert(a, s)
+                                              : launch_output_convert(a, s);
+        break;
+      }
+      case StepKind::ConvWinograd:
+      case StepKind::ConvDirect: {
+        Epilogue epi = st.epi;
+        epi.bias = static_cast<const float*>(wbufs_[st.bbuf].ptr);
+        epi.skip0 = static_cast<const uint16_t*>(ptr(st.skip[0]));
+        epi.skip1 = static_cast<const uint16_t*>(ptr(st.skip[1]));
+        epi.out = ptr(st.out);
+        if (st.kind == StepKind::ConvDirect) {
+          DirectArgs a{};
+          a.in = static_cast<const uint16_t*>(ptr(st.in));
+          a.w = static_cast<const uint16_t*>(wbufs_[st.wbuf].ptr);
+          a.epi = epi;
+          a.N = st.N; a.H = st.H; a.W = st.W; a.M = st.M;
+          e = launch_direct(a, s);
+        } else {
+          WinoArgs a{};
+          a.in = static_cast<const uint16_t*>(ptr(st.in));
+          a.u = static_cast<const uint16_t*>(wbufs_[st.wbuf].ptr);
+          a.epi = epi;
+          a.N = st.N; a.H = st.H; a.W = st.W; a.C = st.C; a.M = st.M;
+          e = launch_winograd(a, s);
+        }
+        break;
+      }
+      case StepKind::Eltwise: {
+        EltArgs a{};
+        a.a = static_cast<const uint16_t*>(ptr(st.in));
+        a.b = static_cast<const uint16_t*>(ptr(st.in2));
+        a.out = static_cast<uint16_t*>(ptr(st.out));
+        a.N = st.N; a.H = st.H; a.W = st.W; a.C = st.C;
+        a.Hp = (int32_t)padded_rows(st.H);
+        a.Wp = (int32_t)padded_cols(st.W);
+        a.op = st.elt_op;
+        a.lo = st.lo;
+        a.hi = st.hi;
+        e = launch_eltwise(a, st.binary, s);
+        break;
+      }
+      case StepKind::DepthToSpace: {
+        DtsArgs a{};
+        a.in = static_cast<const uint16_t*>(ptr(st.in));
+        a.out = ptr(st.out);
+        a.N = st.N; a.H = st.H; a.W = st.W; a.C = st.C;
+        a.Hp = (int32_t)padded_rows(st.H);
+        a.Wp = (int32_t)padded_cols(st.W);
+        a.b = st.dts_b;
+        a.out_kind = st.out_kind;
+        a.do_clip = st.do_clip;
+        a.lo = st.lo;
+        a.hi = st.hi;
+        e = launch_dts(a, s);
+        break;
+      }
+    }
+    if (e != hipSuccess) {
+      error = "HIP kernel launch for step " + std::to_string(i) + " failed: " +
+              hipGetErrorString(e);
+      return false;
+    }
+    if (profiling_) {
+      if (hipEventRecord(ev.stop, s) != hipSuccess) {
+        error = "HIP event record for profiling failed";
+        return false;
+      }
+      pending_events_.push_back(ev);
+    }
+  }
+  return true;
+}
+
+hipEvent_t Engine::TakeEvent() {
+  if (!event_pool_.empty()) {
+    hipEvent_t e = event_pool_.back();
+    event_pool_.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+std::string Engine::StepName(const Step& st) const {
+  static const char* acts[] = {"", " relu", " silu"};
+  std::ostringstream os;
+  switch (st.kind) {
+    case StepKind::InputConvert: os << "input_convert C" << st.C; break;
+    case StepKind::OutputConvert: os << "output_convert C" << st.C; break;
+    case StepKind::ConvWinograd:
+    case StepKind::ConvDirect:
+      os << (st.kind == StepKind::ConvWinograd ? "winograd_conv" : "direct_conv") << " C" << st.C
+         << " M" << st.M << acts[st.epi.act];
+      for (int k = 0; k < 2; ++k)
+        if (st.skip[k] != kNoBuffer) os << " +skip";
+      if (st.epi.dts_b) os << " +dts" << st.epi.dts_b;
+      if (st.epi.do_clip) os << " +clip";
+      break;
+    case StepKind::Eltwise: os << "eltwise op" << st.elt_op << (st.binary ? " binary" : ""); break;
+    case StepKind::DepthToSpace: os << "depth_to_space b" << st.dts_b; break;
+  }
+  os << " [" << st.N << "x" << st.H << "x" << st.W << "]";
+  return os.str();
+}
+
+void Engine::SetProfiling(bool on) {
+  std::lock_guard<std::mutex> lock(mu_);
+  profiling_ = on;
+  prof_acc_.clear();
+}
+
+bool Engine::ProfileRead(std::vector<StepProfile>& out, std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  for (const EventPair& ev : pending_events_) {
+    hipError_t e = hipEventSynchronize(ev.stop);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.start, ev.stop);
+    if (e != hipSuccess) {
+      error = HipErr("hipEventElapsedTime", e);
+      return false;
+    }
+    if (ev.step < static_cast<int>(prof_acc_.size())) {
+      prof_acc_[ev.step].total_ms += ms;
+      prof_acc_[ev.step].launches += 1;
+    }
+    event_pool_.push_back(ev.start);
+    event_pool_.push_back(ev.stop);
+  }
+  pending_events_.clear();
+  out = prof_acc_;
+  for (auto& p : prof_acc_) {
+    p.total_ms = 0.0;
+    p.launches = 0;
+  }
+  return true;
+}
+
+bool Engine::Run(const void* in_host, const int64_t in[4], void* out_host, size_t out_cap,
+                 std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  (void)hipGetLastError();  // a stale error from an earlier failed call is not this run's
+  if (!Init(error)) return false;
+  if (!EnsurePlan(in, error)) return false;
+  if (in_host == nullptr || out_host == nullptr) {
+    error = "null host buffer";
+    return false;
+  }
+  if (out_cap < out_bytes_) {
+    error = "output buffer too small (" + std::to_string(out_cap) + " bytes, need " +
+            std::to_string(out_bytes_) + ")";
+    return false;
+  }
+  hipError_t e;
+  if (in_stage_dev_ == nullptr) {
+    if ((e = hipMalloc(&in_stage_dev_, in_bytes_)) != hipSuccess ||
+        (e = hipMalloc(&out_stage_dev_, out_bytes_)) != hipSuccess ||
+        (e = hipHostMalloc(&in_pinned_, in_bytes_, hipHostMallocDefault)) != hipSuccess ||
+        (e = hipHostMalloc(&out_pinned_, out_bytes_, hipHostMallocDefault)) != hipSuccess) {
+      error = "hipMalloc of IO staging failed: " + std::string(hipGetErrorString(e));
+      FreePlan();
+      return false;
+    }
+  }
+  std::memcpy(in_pinned_, in_host, in_bytes_);
+  if ((e = hipMemcpyAsync(in_stage_dev_, in_pinned_, in_bytes_, hipMemcpyHostToDevice,
+                          stream_)) != hipSuccess) {
+    error = HipErr("HIP input upload", e);
+    return false;
+  }
+  if (!Enqueue(in_stage_dev_, out_stage_dev_, stream_, error)) return false;
+  if ((e = hipMemcpyAsync(out_pinned_, out_stage_dev_, out_bytes_, hipMemcpyDeviceToHost,
+                          stream_)) != hipSuccess) {
+    error = HipErr("HIP output download", e);
+    return false;
+  }
+  if ((e = hipStreamSynchronize(stream_)) != hipSuccess) {
+    error = HipErr("HIP stream synchronize", e);
+    return false;
+  }
+  std::memcpy(out_host, out_pinned_, out_bytes_);
+  return true;
+}
+
+bool Engine::RunDevice(const void* in_dev, const int64_t in[4], void* out_dev,
+                       hipStream_t stream, std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  (void)hipGetLastError();
+  if (!Init(error)) return false;
+  if (!EnsurePlan(in, error)) return false;
+  if (in_dev == nullptr || out_dev == nullptr) {
+    error = "null device buffer";
+    return false;
+  }
+  return Enqueue(in_dev, out_dev, stream ? stream : stream_, error);
+}
+
+std::string Engine::Describe() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  std::ostringstream os;
+  os << "input '" << graph_.input_name << "'" << (graph_.input_fp32 ? " fp32" : " fp16")
+     << ", output '" << graph_.output_name << "'" << (graph_.output_fp32 ? " fp32" : " fp16")
+     << "\n";
+  static const char* acts[] = {"", "+relu", "+silu"};
+  for (size_t i = 0; i < graph_.ops.size(); ++i) {
+    const Op& op = graph_.ops[i];
+    os << "op" << i << " " << OpKindName(op.kind);
+    if (op.kind == OpKind::Conv) {
+      const Weight& w = graph_.weights.at(op.weight);
+      os << " " << w.dims[1] << "->" << w.dims[0] << acts[op.act];
+      for (const auto& s : op.skips) os << " +skip(" << s << ")";
+      if (op.dts_b) os << " +dts" << op.dts_b;
+    }
+    if (op.clip) os << " +clip[" << op.clip_lo << "," << op.clip_hi << "]";
+    os << " : " << op.in0 << (op.in1.empty() ? "" : ", " + op.in1) << " -> " << op.out << "\n";
+  }
+  if (planned_) {
+    os << "plan for [" << plan_in_[0] << "," << plan_in_[1] << "," << plan_in_[2] << ","
+       << plan_in_[3] << "]: " << steps_.size() << " launches, " << bufs_.size()
+       << " activation buffers:";
+    size_t total = 0;
+    for (const auto& b : bufs_) total += b.bytes;
+    os << " " << total << " bytes\n";
+  }
+  return os.str();
+}
+
+}  // namespace arthip

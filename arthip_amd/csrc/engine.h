@@ -1,0 +1,144 @@
+// The conv-chain engine: one compiled model on one GPU.
+//
+// Replaces vship::HipEngine (src/vapoursynth/hip_engine.h:88-188) and
+// onnxruntime::hip::HipGraph (src/onnxruntime-hip/hip_graph.h:113-167) with a
+// single core both adapters can drive: Build parses and fuses an ONNX model;
+// a per-input-shape plan (buffers, packed weights, launch list) is built on
+// first use and cached; Run executes one batch host-to-host, RunDevice on
+// device-resident buffers. Thread-safe through an internal mutex; every entry
+// point re-selects the device (HIP's current device is per thread).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "conv_args.h"
+#include "graph.h"
+
+namespace arthip {
+
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+enum class StepKind { InputConvert, ConvWinograd, ConvDirect, Eltwise, DepthToSpace, OutputConvert };
+
+// Buffer reference inside a plan: an index into Engine::bufs_, or the
+// boundary input/output supplied per run.
+constexpr int kBoundaryIn = -2;
+constexpr int kBoundaryOut = -3;
+constexpr int kNoBuffer = -1;
+
+struct Step {
+  StepKind kind = StepKind::ConvWinograd;
+  int op = -1;  // index into Graph::ops (-1 for IO steps)
+  int in = kNoBuffer, in2 = kNoBuffer, out = kNoBuffer;
+  int skip[2] = {kNoBuffer, kNoBuffer};
+  int wbuf = kNoBuffer, bbuf = kNoBuffer;  // packed weights / padded bias (weight cache)
+  // Geometry of the step's input (NHWC) and channel counts.
+  int32_t N = 0, H = 0, W = 0, C = 0, M = 0;
+  Epilogue epi{};  // conv epilogue (pointers resolved per run)
+  int32_t elt_op = 0;
+  bool binary = false;
+  int32_t dts_b = 0, out_kind = kOutPadded, do_clip = 0;
+  float lo = 0.0f, hi = 0.0f;
+  int32_t fp32 = 0;  // IO steps: boundary side is fp32
+};
+
+class Engine {
+ public:
+  explicit Engine(int device_id);
+  ~Engine();
+  Engine(const Engine&) = delete;
+  Engine& operator=(const Engine&) = delete;
+
+  // Selects the device and creates the engine's stream (once; later calls
+  // only re-select the device). Run / RunDevice call it; Build does not, so
+  // models can be parsed and validated without a GPU.
+  bool Init(std::string& error);
+
+  bool Build(const void* data, size_t size, std::string& error);
+  bool BuildFile(const std::string& path, std::string& error);
+
+  bool OutputShape(const int64_t in_nchw[4], int64_t out_nchw[4]) const;
+  bool InputFp32() const { return graph_.input_fp32; }
+  bool OutputFp32() const { return graph_.output_fp32; }
+  // First conv's input channels / last conv's output channels (before a
+  // trailing DepthToSpace), as the reference reports them (hip_engine.h:127-136).
+  int InputChannels() const;
+  int OutputChannels() const;
+
+  bool Run(const void* in_host, const int64_t in_nchw[4], void* out_host, size_t out_cap,
+           std::string& error);
+  bool RunDevice(const void* in_dev, const int64_t in_nchw[4], void* out_dev, hipStream_t stream,
+                 std::string& error);
+
+  std::string Describe() const;
+
+  // Per-launch GPU timing with HIP events recorded around every step on the
+  // launch stream (the reference's VSHIP_PROFILE, hip_engine.cc:1409-1606).
+  // ProfileRead synchronizes the recorded events and returns, per plan step,
+  // the summed milliseconds and launch count since the last read.
+  void SetProfiling(bool on);
+  struct StepProfile {
+    std::string name;
+    double total_ms = 0.0;
+    int64_t launches = 0;
+  };
+  bool ProfileRead(std::vector<StepProfile>& out, std::string& error);
+  size_t InputBytes(const int64_t in_nchw[4]) const;
+  size_t OutputBytes(const int64_t in_nchw[4]) const;
+
+ private:
+  bool SetDevice(std::string& error) const;
+  bool EnsurePlan(const int64_t in_nchw[4], std::string& error);
+  bool EnsureWeights(std::string& error);
+  bool Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::string& error);
+  void FreePlan();
+  void FreeAll();
+
+  int device_;
+  hipStream_t stream_ = nullptr;
+  Graph graph_;
+  bool built_ = false;
+
+  // Packed weights, shape independent; uploaded on the first plan.
+  bool weights_ready_ = false;
+  std::vector<DevBuf> wbufs_;
+  std::unordered_map<int, int> op_wbuf_, op_bbuf_;  // op index -> wbufs_ index
+
+  // Current plan.
+  bool planned_ = false;
+  int64_t plan_in_[4] = {0, 0, 0, 0};
+  std::vector<DevBuf> bufs_;
+  std::vector<Step> steps_;
+  std::vector<std::string> buf_names_;
+  size_t in_bytes_ = 0, out_bytes_ = 0;
+  // Host Run path: device copies of the boundary tensors and pinned staging.
+  void* in_stage_dev_ = nullptr;
+  void* out_stage_dev_ = nullptr;
+  void* in_pinned_ = nullptr;
+  void* out_pinned_ = nullptr;
+
+  // Profiling: event pairs (step index, start, stop) not yet read.
+  bool profiling_ = false;
+  struct EventPair {
+    int step;
+    hipEvent_t start, stop;
+  };
+  std::vector<EventPair> pending_events_;
+  std::vector<hipEvent_t> event_pool_;
+  std::vector<StepProfile> prof_acc_;
+  hipEvent_t TakeEvent();
+  std::string StepName(const Step& st) const;
+
+  mutable std::mutex mu_;
+};
+
+}  // namespace arthip

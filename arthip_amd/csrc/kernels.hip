@@ -5,30 +5,32 @@
 // (direct_conv 402-483), DepthToSpace (dts_kernel* 532-616), the unfused
 // pointwise ops (unary_kernel/binary_kernel 493-519) and the NCHW<->NHWC IO
 // kernels (629-670). Written for 64-wide wavefronts and the
-// v_mfma_f32_16x16x32_f16 matrix instruction; nothing here is shared with the
+// v_mfma_f32_16x16x32_f16 matrix instruction; nothing here follows the
 // reference's wave32 WMMA design.
 //
-// winograd_conv data flow (F(2x2,3x3), one persistent workgroup per slot):
+// winograd_conv data flow (F(2x2,3x3), persistent workgroups):
 //   * Each wave owns one 16-wide block of output channels and keeps its share
 //     of the transformed filters U' (16 positions x C x 16 outputs, fp16) in
-//     VGPRs for the whole launch, so U is read from HBM/L2 once per workgroup.
-//   * Per work item (1 tile row x 16*tb tile columns): all threads load 4x4
-//     input patches (4 channels per lane, NHWC fp16, zero padded), apply
-//     V' = (B^T d B)/4 in packed fp16 and write V' to LDS as
-//     [position][tile][channel] with a 16-byte row pad (conflict-free 16-byte
-//     reads for the MFMA B operand).
+//     VGPRs for the whole launch, so U' is read from HBM/L2 once per workgroup.
+//   * Per work item (1 tile row x 16*tb tile columns) every thread owns input
+//     tasks of one tile x 4 channels: it loads the 4x4 patch from the padded
+//     NHWC input (no bounds checks), applies V' = (B^T d B)/4 in packed fp16
+//     and writes V' to LDS as [position][tile][channel] with a 16-byte row pad
+//     (conflict-free 16-byte reads for the MFMA B operand). When each thread
+//     has exactly one task, the next item's patch is loaded into registers
+//     while the current item runs on the matrix cores.
 //   * Each wave runs, per position, KC chained MFMAs over 32-channel chunks
 //     (A = U' rows = output channels, B = V' columns = tiles) and folds the
 //     16 position results into the 2x2 output tile with A^T M A in fp32.
-//   * Epilogue in fp32: bias, ReLU/SiLU, up to two residual inputs, Clip, one
-//     rounding; stores NHWC fp16, or the NCHW boundary layout (fp16/fp32),
-//     optionally through a fused DepthToSpace.
+//   * Epilogue: bias, ReLU/SiLU, up to two residual inputs, Clip; stores the
+//     padded NHWC layout, or the NCHW boundary layout (fp16/fp32), optionally
+//     through a fused DepthToSpace.
 //
 // Scaling: V is computed as (B^T d B)/4 (exact in fp16 away from subnormals)
-// so that |V'| <= max|d| never overflows fp16; the host packs U' = 4*U to
-// compensate. Column-3 positions come out with the opposite sign (that keeps
-// the scaled transform at one fused multiply-add per value); the output fold
-// absorbs the sign, so U' is not negated.
+// so that |V'| <= 2 max|d| never overflows fp16 where d does not; the host packs
+// U' = 4*U to compensate. Column-3 positions come out with the opposite sign
+// (that keeps the scaled transform at one fused multiply-add per value); the
+// output fold absorbs the sign, so U' is not negated.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -62,12 +64,31 @@ __device__ __forceinline__ float apply_clip(float y, float lo, float hi) {
   return (y < lo) ? lo : ((y > hi) ? hi : y);
 }
 
-// Epilogue for 4 consecutive output channels [ch0, ch0+4) of one pixel.
-// ch0 is a multiple of 4 and ch0 < M; lanes for channels >= M keep out.
-__device__ __forceinline__ void store4(const Epilogue& e, int M, int H, int W, int n, int oh,
-                                       int ow, int ch0, f4 v) {
-  const int64_t pix = ((int64_t)n * H + oh) * W + ow;
-  const bool vec = (M & 3) == 0;  // then ch0 + 3 < M
+__device__ __forceinline__ h4 to_h4(f4 v) {
+  return h4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+}
+
+// Invariant-divisor division for the persistent work-item index (uniform
+// values; avoids the long scalar division sequence). Valid for x < 2^31.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
+  const uint64_t t = (static_cast<uint64_t>(x) * f.m) >> 32;
+  return static_cast<uint32_t>((t + x) >> f.s);
+}
+
+// ---------------------------------------------------------------------------
+// Epilogues
+// ---------------------------------------------------------------------------
+
+// General epilogue for 4 consecutive output channels [ch0, ch0+4) of pixel
+// (oh, ow); fp32 until one final rounding. ch0 % 4 == 0 and ch0 < M.
+__device__ __forceinline__ void store4(const Epilogue& e, int M, int H, int W, int Hp, int Wp,
+                                       int n, int oh, int ow, int ch0, f4 v) {
+  const int64_t ppix = ((int64_t)n * Hp + oh + 1) * Wp + ow + 1;  // padded pixel
+  const bool vec = (M & 3) == 0;                                  // then ch0 + 3 < M
   v += *reinterpret_cast<const f4*>(e.bias + ch0);
 #pragma unroll
   for (int q = 0; q < 4; ++q) v[q] = apply_act(v[q], e.act);
@@ -76,7 +97,7 @@ __device__ __forceinline__ void store4(const Epilogue& e, int M, int H, int W, i
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (sk[s] == nullptr) continue;
-    const _Float16* p = sk[s] + pix * M + ch0;
+    const _Float16* p = sk[s] + ppix * M + ch0;
     if (vec) {
       const h4 x = *reinterpret_cast<const h4*>(p);
 #pragma unroll
@@ -114,13 +135,10 @@ __device__ __forceinline__ void store4(const Epilogue& e, int M, int H, int W, i
     }
     return;
   }
-  if (e.out_kind == kOutNhwcF16) {
-    _Float16* o = reinterpret_cast<_Float16*>(e.out) + pix * M + ch0;
+  if (e.out_kind == kOutPadded) {
+    _Float16* o = reinterpret_cast<_Float16*>(e.out) + ppix * M + ch0;
     if (vec) {
-      h4 r;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) r[q] = (_Float16)v[q];
-      *reinterpret_cast<h4*>(o) = r;
+      *reinterpret_cast<h4*>(o) = to_h4(v);
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -128,7 +146,6 @@ __device__ __forceinline__ void store4(const Epilogue& e, int M, int H, int W, i
     }
     return;
   }
-  // NCHW boundary layout.
   const int64_t plane = (int64_t)H * W;
   const int64_t base = ((int64_t)n * M + ch0) * plane + (int64_t)oh * W + ow;
 #pragma unroll
@@ -141,33 +158,55 @@ __device__ __forceinline__ void store4(const Epilogue& e, int M, int H, int W, i
   }
 }
 
+// Fast epilogue for 4 channels of one pixel: round acc + bias to fp16, then
+// act and the residual adds in packed fp16. s0/s1 are zero when absent.
+template <int ACT>
+__device__ __forceinline__ h4 fast4(f4 y, f4 bias4, h4 s0, h4 s1) {
+  h4 r = to_h4(y + bias4);
+  if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
+  if (ACT == kActSilu) {
+    f4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = (float)r[e];
+      t[e] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    }
+    r = to_h4(t);
+  }
+  r += s0;
+  r += s1;
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // Winograd F(2x2,3x3)
 // ---------------------------------------------------------------------------
 
-// 4x4 input patch with top-left input pixel (h0, w0), channels [c0, c0+4).
-// Out-of-image pixels and channels >= C read as zero (SAME padding and the
-// channel padding of the last 32-channel chunk).
-__device__ __forceinline__ void load_patch(const WinoArgs& a, int n, int h0, int w0, int c0,
-                                           h4 d[16]) {
-  const _Float16* in = reinterpret_cast<const _Float16*>(a.in);
-  const bool cvec = (a.C & 3) == 0;
+// 4x4 patch of input task `task` (tile t of the item, channel quad c0) from
+// the padded input; tasks past the last tile column or channel read as zero.
+template <int KC, bool CVEC>
+__device__ __forceinline__ void load_task(const WinoArgs& a, int n, int th, int tw0, int task,
+                                          h4 d[16]) {
+  constexpr int QUADS = KC * 8;
+  const int t = task / QUADS;
+  const int c0 = (task - t * QUADS) * 4;
+  const bool ok = (tw0 + t < a.tiles_w) && (c0 < a.C);
+  const _Float16* p = reinterpret_cast<const _Float16*>(a.in) +
+                      (((int64_t)n * a.Hp + 2 * th) * a.Wp + 2 * (tw0 + t)) * a.C + c0;
+  const int64_t rs = (int64_t)a.Wp * a.C;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int h = h0 + i;
-    const bool hok = (h >= 0) && (h < a.H);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int w = w0 + j;
       h4 v = {0, 0, 0, 0};
-      if (hok && w >= 0 && w < a.W && c0 < a.C) {
-        const _Float16* p = in + (((int64_t)n * a.H + h) * a.W + w) * a.C + c0;
-        if (cvec) {
-          v = *reinterpret_cast<const h4*>(p);
+      if (ok) {
+        const _Float16* q = p + i * rs + j * a.C;
+        if (CVEC) {
+          v = *reinterpret_cast<const h4*>(q);
         } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (c0 + q < a.C) v[q] = p[q];
+          for (int e = 0; e < 4; ++e)
+            if (c0 + e < a.C) v[e] = q[e];
         }
       }
       d[i * 4 + j] = v;
@@ -175,34 +214,62 @@ __device__ __forceinline__ void load_patch(const WinoArgs& a, int n, int h0, int
   }
 }
 
-// V' for positions p = 4*i + j: V'_{i,j} = (B^T d B)_{i,j} / 4 for j < 3 and
-// -(B^T d B)_{i,3} / 4 for j == 3, with B^T = [[1,0,-1,0],[0,1,1,0],
-// [0,-1,1,0],[0,1,0,-1]]. First stage (columns) in plain fp16; the second
-// stage folds the 1/4 into one fma per value.
-__device__ __forceinline__ void input_transform(const h4 d[16], h4 v[16]) {
-  h4 t[16];
+// Writes V' of one task: V'_{i,j} = (B^T d B)_{i,j}/4 for j < 3 and
+// -(B^T d B)_{i,3}/4, with B^T = [[1,0,-1,0],[0,1,1,0],[0,-1,1,0],[0,1,0,-1]].
+// First stage (columns) in plain fp16; the second stage folds the 1/4 into one
+// fma per value and streams each output row to LDS.
+template <int KC>
+__device__ __forceinline__ void store_v(_Float16* vlds, int wps, int task, const h4 d[16]) {
+  constexpr int TS = KC * 32 + 8;
+  constexpr int QUADS = KC * 8;
+  const int t = task / QUADS;
+  const int c0 = (task - t * QUADS) * 4;
+  _Float16* dst = vlds + t * TS + c0;
+  h4 tt[16];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    t[0 * 4 + j] = d[0 * 4 + j] - d[2 * 4 + j];
-    t[1 * 4 + j] = d[1 * 4 + j] + d[2 * 4 + j];
-    t[2 * 4 + j] = d[2 * 4 + j] - d[1 * 4 + j];
-    t[3 * 4 + j] = d[1 * 4 + j] - d[3 * 4 + j];
+    tt[0 * 4 + j] = d[0 * 4 + j] - d[2 * 4 + j];
+    tt[1 * 4 + j] = d[1 * 4 + j] + d[2 * 4 + j];
+    tt[2 * 4 + j] = d[2 * 4 + j] - d[1 * 4 + j];
+    tt[3 * 4 + j] = d[1 * 4 + j] - d[3 * 4 + j];
   }
   const h4 qp = {0.25f16, 0.25f16, 0.25f16, 0.25f16};
   const h4 qn = {-0.25f16, -0.25f16, -0.25f16, -0.25f16};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const h4 n1 = t[i * 4 + 1] * qn;
-    const h4 n2 = t[i * 4 + 2] * qn;
-    v[i * 4 + 0] = __builtin_elementwise_fma(t[i * 4 + 0], qp, n2);   // (t0 - t2)/4
-    v[i * 4 + 1] = __builtin_elementwise_fma(t[i * 4 + 1], qp, -n2);  // (t1 + t2)/4
-    v[i * 4 + 2] = __builtin_elementwise_fma(t[i * 4 + 2], qp, n1);   // (t2 - t1)/4
-    v[i * 4 + 3] = __builtin_elementwise_fma(t[i * 4 + 3], qp, n1);   // (t3 - t1)/4
+    const h4 n1 = tt[i * 4 + 1] * qn;
+    const h4 n2 = tt[i * 4 + 2] * qn;
+    _Float16* row = dst + (i * 4) * wps;
+    *reinterpret_cast<h4*>(row) = __builtin_elementwise_fma(tt[i * 4 + 0], qp, n2);
+    *reinterpret_cast<h4*>(row + wps) = __builtin_elementwise_fma(tt[i * 4 + 1], qp, -n2);
+    *reinterpret_cast<h4*>(row + 2 * wps) = __builtin_elementwise_fma(tt[i * 4 + 2], qp, n1);
+    *reinterpret_cast<h4*>(row + 3 * wps) = __builtin_elementwise_fma(tt[i * 4 + 3], qp, n1);
   }
 }
 
-template <int KC>
-__global__ void __launch_bounds__(512) winograd_conv(WinoArgs a) {
+struct WinoSched {
+  FastDiv sb_w, tiles_h;
+};
+
+// Item index -> (n, tile row, first tile column).
+__device__ __forceinline__ void item_coords(const WinoSched& sc, int sb, int ntile, int& n,
+                                            int& th, int& tw0) {
+  const uint32_t rest = fdiv((uint32_t)sb, sc.sb_w);
+  const uint32_t tws = (uint32_t)sb - rest * sc.sb_w.d;
+  const uint32_t nn = fdiv(rest, sc.tiles_h);
+  th = (int)(rest - nn * sc.tiles_h.d);
+  n = (int)nn;
+  tw0 = (int)tws * ntile;
+}
+
+// KC:    32-channel input chunks (C <= 32*KC); U' of this wave lives in VGPRs.
+// CVEC:  C % 4 == 0 (8-byte input loads).
+// FAST:  padded NHWC output with M % 4 == 0 and no clip (the inner layers);
+//        else the general epilogue (boundary layouts, fused DepthToSpace, odd M).
+// PF:    exactly one input task per thread: the next item's patch is
+//        prefetched into registers while the current item runs on MFMA.
+template <int KC, bool CVEC, bool FAST, bool PF>
+__global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
   extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
   constexpr int CP = KC * 32;  // padded input channels
   constexpr int TS = CP + 8;   // LDS halfs per tile row (16-byte pad)
@@ -214,6 +281,17 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a) {
   const int tbi = wave / a.n_ob;
   const int ntile = 16 * a.tb;
   const int wps = ntile * TS;  // LDS halfs per position
+  const int ntask = ntile * QUADS;
+
+  // Persistent schedule. Workgroups are dispatched round-robin over the 8
+  // XCDs, so workgroup id % 8 is its XCD; each XCD walks one contiguous band
+  // of work items so that vertically adjacent tile rows (which share input
+  // halo rows) meet in the same L2. gridDim.x is a multiple of 8.
+  const int xcd = blockIdx.x & 7;
+  const int nslot = gridDim.x >> 3;
+  const int sb_end = (int)(((int64_t)a.n_sb * (xcd + 1)) >> 3);
+  int sb = (int)(((int64_t)a.n_sb * xcd) >> 3) + (blockIdx.x >> 3);
+  if (sb >= sb_end) return;  // uniform across the workgroup
 
   // This wave's U' slice, laid out by the host in MFMA A-operand order:
   // [ob][position][kc][lane][8 halfs].
@@ -226,41 +304,66 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a) {
       for (int kc = 0; kc < KC; ++kc) u[p][kc] = up[(p * KC + kc) * 64];
   }
 
-  // Persistent schedule. Workgroups are dispatched round-robin over the 8
-  // XCDs, so workgroup id % 8 is its XCD; each XCD walks one contiguous band
-  // of work items so that vertically adjacent tile rows (which share input
-  // halo rows) meet in the same L2. gridDim.x is a multiple of 8.
-  const int xcd = blockIdx.x & 7;
-  const int slot = blockIdx.x >> 3;
-  const int nslot = gridDim.x >> 3;
-  const int sb_begin = (int)(((int64_t)a.n_sb * xcd) >> 3);
-  const int sb_end = (int)(((int64_t)a.n_sb * (xcd + 1)) >> 3);
-  const int ntask = ntile * QUADS;
+  // Lane's output coordinates within an item: 4 channels x one tile.
+  const int ch0 = ob * 16 + 4 * (lane >> 4);
+  const int tcol = tbi * 16 + (lane & 15);
+  f4 bias4 = {0, 0, 0, 0};
+  if (FAST && ch0 < a.M) bias4 = *reinterpret_cast<const f4*>(a.epi.bias + ch0);
 
-  for (int sb = sb_begin + slot; sb < sb_end; sb += nslot) {
-    const int tws = sb % a.sb_w;
-    const int rest = sb / a.sb_w;
-    const int th = rest % a.tiles_h;
-    const int n = rest / a.tiles_h;
-    const int tw0 = tws * ntile;
+  int n, th, tw0;
+  item_coords(sc, sb, ntile, n, th, tw0);
+  h4 d[16];
+  if (PF) load_task<KC, CVEC>(a, n, th, tw0, tid, d);
 
+  for (;;) {
     // ---- input transform into LDS
-    for (int task = tid; task < ntask; task += blockDim.x) {
-      const int t = task / QUADS;
-      const int c0 = (task - t * QUADS) * 4;
-      h4 d[16];
-      load_patch(a, n, 2 * th - 1, 2 * (tw0 + t) - 1, c0, d);
-      h4 v[16];
-      input_transform(d, v);
-      _Float16* dst = vlds + t * TS + c0;
-#pragma unroll
-      for (int p = 0; p < 16; ++p) *reinterpret_cast<h4*>(dst + p * wps) = v[p];
+    if (PF) {
+      store_v<KC>(vlds, wps, tid, d);
+    } else {
+      for (int task = tid; task < ntask; task += blockDim.x) {
+        load_task<KC, CVEC>(a, n, th, tw0, task, d);
+        store_v<KC>(vlds, wps, task, d);
+      }
     }
     lds_sync();
 
+    const int nsb = sb + nslot;
+    const bool more = nsb < sb_end;
+    int nn = n, nth = th, ntw0 = tw0;
+    if (more) item_coords(sc, nsb, ntile, nn, nth, ntw0);
+    if (PF && more) load_task<KC, CVEC>(a, nn, nth, ntw0, tid, d);
+
+    const int tw = tw0 + tcol;
+    const bool valid = (ch0 < a.M) && (tw < a.tiles_w);
+    const int oh = 2 * th, ow = 2 * tw;
+    const bool h1 = oh + 1 < a.H, w1 = ow + 1 < a.W;
+    const int64_t ppix = ((int64_t)n * a.Hp + oh + 1) * a.Wp + ow + 1;
+    const int64_t prow = (int64_t)a.Wp * a.M;
+    // Residual inputs for the fast epilogue, requested before the MFMA work.
+    h4 sk[2][4];
+    if (FAST) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const _Float16* sp = reinterpret_cast<const _Float16*>(s == 0 ? a.epi.skip0 : a.epi.skip1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sk[s][q] = h4{0, 0, 0, 0};
+        if (sp != nullptr && valid) {
+          const _Float16* b = sp + ppix * a.M + ch0;
+          sk[s][0] = *reinterpret_cast<const h4*>(b);
+          if (w1) sk[s][1] = *reinterpret_cast<const h4*>(b + a.M);
+          if (h1) {
+            sk[s][2] = *reinterpret_cast<const h4*>(b + prow);
+            if (w1) sk[s][3] = *reinterpret_cast<const h4*>(b + prow + a.M);
+          }
+        }
+      }
+    }
+
     // ---- 16 position GEMMs on MFMA, folded row by row into the 2x2 tile
-    f4 y00 = {0, 0, 0, 0}, y01 = y00, y10 = y00, y11 = y00;
-    const _Float16* vb = vlds + (tbi * 16 + (lane & 15)) * TS + (lane >> 4) * 8;
+    f4 y[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = f4{0, 0, 0, 0};
+    const _Float16* vb = vlds + tcol * TS + (lane >> 4) * 8;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       f4 m0 = {0, 0, 0, 0}, m1 = m0, m2 = m0, m3 = m0;
@@ -281,41 +384,57 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a) {
       const f4 s0 = m0 + m1 + m2;
       const f4 s1 = m1 - m2 + m3;
       if (r == 0) {
-        y00 += s0;
-        y01 += s1;
+        y[0] += s0;
+        y[1] += s1;
       } else if (r == 1) {
-        y00 += s0;
-        y01 += s1;
-        y10 += s0;
-        y11 += s1;
+        y[0] += s0;
+        y[1] += s1;
+        y[2] += s0;
+        y[3] += s1;
       } else if (r == 2) {
-        y00 += s0;
-        y01 += s1;
-        y10 -= s0;
-        y11 -= s1;
+        y[0] += s0;
+        y[1] += s1;
+        y[2] -= s0;
+        y[3] -= s1;
       } else {
-        y10 -= s0;
-        y11 -= s1;
+        y[2] -= s0;
+        y[3] -= s1;
       }
     }
 
-    // ---- epilogue: lane holds 4 channels x 4 pixels of one tile
-    {
-      const int ch0 = ob * 16 + 4 * (lane >> 4);
-      const int tw = tw0 + tbi * 16 + (lane & 15);
-      if (ch0 < a.M && tw < a.tiles_w) {
-        const int oh = 2 * th;
-        const int ow = 2 * tw;
-        const bool w1 = ow + 1 < a.W;
-        store4(a.epi, a.M, a.H, a.W, n, oh, ow, ch0, y00);
-        if (w1) store4(a.epi, a.M, a.H, a.W, n, oh, ow + 1, ch0, y01);
-        if (oh + 1 < a.H) {
-          store4(a.epi, a.M, a.H, a.W, n, oh + 1, ow, ch0, y10);
-          if (w1) store4(a.epi, a.M, a.H, a.W, n, oh + 1, ow + 1, ch0, y11);
+    // ---- epilogue: lane holds 4 channels x the 4 pixels of one tile
+    if (valid) {
+      if (FAST) {
+        _Float16* o = reinterpret_cast<_Float16*>(a.epi.out) + ppix * a.M + ch0;
+        const int64_t off[4] = {0, a.M, prow, prow + a.M};
+        const bool ok[4] = {true, w1, h1, h1 && w1};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (!ok[q]) continue;
+          h4 r;
+          if (a.epi.act == kActRelu)
+            r = fast4<kActRelu>(y[q], bias4, sk[0][q], sk[1][q]);
+          else if (a.epi.act == kActSilu)
+            r = fast4<kActSilu>(y[q], bias4, sk[0][q], sk[1][q]);
+          else
+            r = fast4<kActNone>(y[q], bias4, sk[0][q], sk[1][q]);
+          *reinterpret_cast<h4*>(o + off[q]) = r;
+        }
+      } else {
+        store4(a.epi, a.M, a.H, a.W, a.Hp, a.Wp, n, oh, ow, ch0, y[0]);
+        if (w1) store4(a.epi, a.M, a.H, a.W, a.Hp, a.Wp, n, oh, ow + 1, ch0, y[1]);
+        if (h1) {
+          store4(a.epi, a.M, a.H, a.W, a.Hp, a.Wp, n, oh + 1, ow, ch0, y[2]);
+          if (w1) store4(a.epi, a.M, a.H, a.W, a.Hp, a.Wp, n, oh + 1, ow + 1, ch0, y[3]);
         }
       }
     }
     lds_sync();  // V' of this item is dead before the next item overwrites it
+    if (!more) break;
+    sb = nsb;
+    n = nn;
+    th = nth;
+    tw0 = ntw0;
   }
 }
 
@@ -326,6 +445,7 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a) {
 // Each thread owns 8 output channels (g = thread % g8) for the whole launch and
 // keeps their 9 taps (as 5 half2 pairs, the 10th tap zero) in VGPRs; the 9 input
 // pixels are multiplied with v_dot2_f32_f16 (fp16 products, fp32 sums).
+template <bool FAST>
 __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
   const int g = threadIdx.x & (a.g8 - 1);
   const int ppb = blockDim.x / a.g8;
@@ -340,6 +460,11 @@ __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
 #pragma unroll
       for (int k = 0; k < 5; ++k) wr[c][k] = wp[c * 5 + k];
   }
+  f4 b0 = {0, 0, 0, 0}, b1 = b0;
+  if (FAST) {
+    b0 = *reinterpret_cast<const f4*>(a.epi.bias + ch0);
+    b1 = *reinterpret_cast<const f4*>(a.epi.bias + ch0 + 4);
+  }
   const _Float16* in = reinterpret_cast<const _Float16*>(a.in);
   const int64_t npix = (int64_t)a.N * a.H * a.W;
   const int64_t step = (int64_t)gridDim.x * ppb;
@@ -348,18 +473,13 @@ __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
     const int64_t rest = p / a.W;
     const int oh = (int)(rest % a.H);
     const int n = (int)(rest / a.H);
+    // Window rows oh..oh+2, columns ow..ow+2 in padded coordinates.
+    const _Float16* src = in + ((int64_t)n * a.Hp + oh) * a.Wp + ow;
     _Float16 x[10];
 #pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      const int h = oh + r - 1;
+    for (int r = 0; r < 3; ++r)
 #pragma unroll
-      for (int s = 0; s < 3; ++s) {
-        const int w = ow + s - 1;
-        x[r * 3 + s] = (h >= 0 && h < a.H && w >= 0 && w < a.W)
-                           ? in[((int64_t)n * a.H + h) * a.W + w]
-                           : (_Float16)0.0f;
-      }
-    }
+      for (int s = 0; s < 3; ++s) x[r * 3 + s] = src[(int64_t)r * a.Wp + s];
     x[9] = (_Float16)0.0f;
     h2 xv[5];
 #pragma unroll
@@ -376,8 +496,156 @@ __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
       acc0[c] = s0;
       acc1[c] = s1;
     }
-    store4(a.epi, a.M, a.H, a.W, n, oh, ow, ch0, acc0);
-    if (ch0 + 4 < a.M) store4(a.epi, a.M, a.H, a.W, n, oh, ow, ch0 + 4, acc1);
+    if (FAST) {
+      const int64_t o = (((int64_t)n * a.Hp + oh + 1) * a.Wp + ow + 1) * a.M + ch0;
+      h4 s00 = {0, 0, 0, 0}, s01 = s00, s10 = s00, s11 = s00;
+      if (a.epi.skip0) {
+        const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip0) + o;
+        s00 = *reinterpret_cast<const h4*>(sp);
+        s01 = *reinterpret_cast<const h4*>(sp + 4);
+      }
+      if (a.epi.skip1) {
+        const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip1) + o;
+        s10 = *reinterpret_cast<const h4*>(sp);
+        s11 = *reinterpret_cast<const h4*>(sp + 4);
+      }
+      h4 r0, r1;
+      if (a.epi.act == kActRelu) {
+        r0 = fast4<kActRelu>(acc0, b0, s00, s10);
+        r1 = fast4<kActRelu>(acc1, b1, s01, s11);
+      } else if (a.epi.act == kActSilu) {
+        r0 = fast4<kActSilu>(acc0, b0, s00, s10);
+        r1 = fast4<kActSilu>(acc1, b1, s01, s11);
+      } else {
+        r0 = fast4<kActNone>(acc0, b0, s00, s10);
+        r1 = fast4<kActNone>(acc1, b1, s01, s11);
+      }
+      h8 r = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+      *reinterpret_cast<h8*>(reinterpret_cast<_Float16*>(a.epi.out) + o) = r;
+    } else {
+      store4(a.epi, a.M, a.H, a.W, a.Hp, a.Wp, n, oh, ow, ch0, acc0);
+      if (ch0 + 4 < a.M) store4(a.epi, a.M, a.H, a.W, a.Hp, a.Wp, n, oh, ow, ch0 + 4, acc1);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise, DepthToSpace and boundary IO (off the fused hot path)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int64_t padded_index(int64_t i, int H, int W, int C, int Hp, int Wp) {
+  const int c = (int)(i % C);
+  int64_t r = i / C;
+  const int w = (int)(r % W);
+  r /= W;
+  const int h = (int)(r % H);
+  const int64_t n = r / H;
+  return ((n * Hp + h + 1) * Wp + w + 1) * C + c;
+}
+
+// Unary (Sigmoid / Relu / Clip) and binary (Add / Mul) ops over the interior
+// of padded tensors; fp32 math, one rounding (hip_kernels.h:493-519).
+__global__ void __launch_bounds__(256) eltwise_kernel(EltArgs a, int binary) {
+  const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  const _Float16* x = reinterpret_cast<const _Float16*>(a.a);
+  const _Float16* y = reinterpret_cast<const _Float16*>(a.b);
+  _Float16* o = reinterpret_cast<_Float16*>(a.out);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = padded_index(i, a.H, a.W, a.C, a.Hp, a.Wp);
+    const float v = (float)x[k];
+    float r;
+    if (binary) {
+      const float w = (float)y[k];
+      r = (a.op == kBinaryMul) ? v * w : v + w;
+    } else if (a.op == kUnarySigmoid) {
+      r = __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+    } else if (a.op == kUnaryRelu) {
+      r = (v < 0.0f) ? 0.0f : v;
+    } else {
+      r = apply_clip(v, a.lo, a.hi);
+    }
+    o[k] = (_Float16)r;
+  }
+}
+
+// DepthToSpace DCR (hip_kernels.h:521-580): output (n, oh, ow, c) reads input
+// channel (r*b + q)*Cout + c at (oh/b, ow/b), r = oh % b, q = ow % b.
+__global__ void __launch_bounds__(256) dts_kernel(DtsArgs a) {
+  const int b = a.b;
+  const int cout = a.C / (b * b);
+  const int Ho = a.H * b, Wo = a.W * b;
+  const int64_t total = (int64_t)a.N * Ho * Wo * cout;
+  const int64_t Hpo = padded_rows(Ho), Wpo = padded_cols(Wo);
+  const _Float16* in = reinterpret_cast<const _Float16*>(a.in);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    // i enumerates the output in its own layout order.
+    int n, c, oh, ow;
+    if (a.out_kind == kOutPadded) {
+      c = (int)(i % cout);
+      int64_t r = i / cout;
+      ow = (int)(r % Wo);
+      r /= Wo;
+      oh = (int)(r % Ho);
+      n = (int)(r / Ho);
+    } else {
+      ow = (int)(i % Wo);
+      int64_t r = i / Wo;
+      oh = (int)(r % Ho);
+      r /= Ho;
+      c = (int)(r % cout);
+      n = (int)(r / cout);
+    }
+    const int h = oh / b, rr = oh - h * b, w = ow / b, q = ow - w * b;
+    const int cin = (rr * b + q) * cout + c;
+    float v = (float)in[(((int64_t)n * a.Hp + h + 1) * a.Wp + w + 1) * a.C + cin];
+    if (a.do_clip) v = apply_clip(v, a.lo, a.hi);
+    if (a.out_kind == kOutPadded)
+      reinterpret_cast<_Float16*>(a.out)[(((int64_t)n * Hpo + oh + 1) * Wpo + ow + 1) * cout + c] =
+          (_Float16)v;
+    else if (a.out_kind == kOutNchwF32)
+      reinterpret_cast<float*>(a.out)[i] = v;
+    else
+      reinterpret_cast<_Float16*>(a.out)[i] = (_Float16)v;
+  }
+}
+
+// Boundary NCHW (fp16 or fp32) -> padded NHWC fp16 (fp32 rounds to nearest
+// even). One thread per NCHW element, so reads are coalesced.
+__global__ void __launch_bounds__(256) input_convert(IoArgs a) {
+  const int64_t total = (int64_t)a.N * a.C * a.H * a.W;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int w = (int)(i % a.W);
+    int64_t r = i / a.W;
+    const int h = (int)(r % a.H);
+    r /= a.H;
+    const int c = (int)(r % a.C);
+    const int64_t n = r / a.C;
+    const _Float16 v = a.fp32 ? (_Float16)reinterpret_cast<const float*>(a.src)[i]
+                              : reinterpret_cast<const _Float16*>(a.src)[i];
+    reinterpret_cast<_Float16*>(a.dst)[((n * a.Hp + h + 1) * a.Wp + w + 1) * a.C + c] = v;
+  }
+}
+
+// Padded NHWC fp16 -> boundary NCHW (fp16 or fp32).
+__global__ void __launch_bounds__(256) output_convert(IoArgs a) {
+  const int64_t total = (int64_t)a.N * a.C * a.H * a.W;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int w = (int)(i % a.W);
+    int64_t r = i / a.W;
+    const int h = (int)(r % a.H);
+    r /= a.H;
+    const int c = (int)(r % a.C);
+    const int64_t n = r / a.C;
+    const _Float16 v =
+        reinterpret_cast<const _Float16*>(a.src)[((n * a.Hp + h + 1) * a.Wp + w + 1) * a.C + c];
+    if (a.fp32)
+      reinterpret_cast<float*>(a.dst)[i] = (float)v;
+    else
+      reinterpret_cast<_Float16*>(a.dst)[i] = v;
   }
 }
 
@@ -400,28 +668,41 @@ int cu_count() {
   return g_cu_count;
 }
 
-template <int KC>
-hipError_t launch_wino_kc(const WinoArgs& a, int threads, size_t lds, int grid, hipStream_t s) {
-  auto fn = winograd_conv<KC>;
-  if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-  }
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), lds, s, a);
-  return hipGetLastError();
+FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0, 0};
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  f.s = s;
+  f.m = static_cast<uint32_t>(((1ull << 32) * ((1ull << s) - d)) / d + 1);
+  return f;
 }
 
+using WinoKernel = void (*)(WinoArgs, WinoSched);
+
 template <int KC>
-int wino_occupancy(int threads, size_t lds) {
-  int blocks = 0;
-  auto fn = winograd_conv<KC>;
-  if (lds > 65536)
-    hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, threads, lds) != hipSuccess)
-    blocks = 1;
-  return blocks < 1 ? 1 : blocks;
+WinoKernel pick_kernel(bool cvec, bool fast, bool pf) {
+  if (cvec) {
+    if (fast) return pf ? winograd_conv<KC, true, true, true> : winograd_conv<KC, true, true, false>;
+    return pf ? winograd_conv<KC, true, false, true> : winograd_conv<KC, true, false, false>;
+  }
+  if (fast) return pf ? winograd_conv<KC, false, true, true> : winograd_conv<KC, false, true, false>;
+  return pf ? winograd_conv<KC, false, false, true> : winograd_conv<KC, false, false, false>;
+}
+
+WinoKernel wino_kernel(int kc, bool cvec, bool fast, bool pf) {
+  switch (kc) {
+    case 1: return pick_kernel<1>(cvec, fast, pf);
+    case 2: return pick_kernel<2>(cvec, fast, pf);
+    case 3: return pick_kernel<3>(cvec, fast, pf);
+    default: return nullptr;
+  }
+}
+
+int grid_for(int64_t total, int threads) {
+  int64_t blocks = (total + threads - 1) / threads;
+  const int64_t cap = (int64_t)cu_count() * 16;
+  if (blocks > cap) blocks = cap;
+  return blocks < 1 ? 1 : (int)blocks;
 }
 
 }  // namespace
@@ -449,25 +730,32 @@ hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
   a.tb = g.tb;
   a.tiles_h = (a.H + 1) / 2;
   a.tiles_w = (a.W + 1) / 2;
+  a.Hp = (int32_t)padded_rows(a.H);
+  a.Wp = (int32_t)padded_cols(a.W);
   a.sb_w = (a.tiles_w + 16 * g.tb - 1) / (16 * g.tb);
   a.n_sb = a.N * a.tiles_h * a.sb_w;
-  int occ = 1;
-  switch (g.kc) {
-    case 1: occ = wino_occupancy<1>(g.threads, g.lds); break;
-    case 2: occ = wino_occupancy<2>(g.threads, g.lds); break;
-    case 3: occ = wino_occupancy<3>(g.threads, g.lds); break;
-    default: return hipErrorInvalidValue;
+  WinoSched sc{make_fastdiv((uint32_t)a.sb_w), make_fastdiv((uint32_t)a.tiles_h)};
+  const bool cvec = (a.C % 4) == 0;
+  const bool fast = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && (a.M % 4) == 0 &&
+                    !a.epi.do_clip;
+  const bool pf = 16 * g.tb * g.kc * 8 == g.threads;  // one input task per thread
+  WinoKernel fn = wino_kernel(g.kc, cvec, fast, pf);
+  if (fn == nullptr) return hipErrorInvalidValue;
+  if (g.lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);
+    if (e != hipSuccess) return e;
   }
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, g.threads, g.lds) != hipSuccess ||
+      occ < 1)
+    occ = 1;
   int grid = cu_count() * occ;
   const int need = (a.n_sb + 7) / 8 * 8;
   if (grid > need) grid = need;
   grid = (grid + 7) / 8 * 8;
-  switch (g.kc) {
-    case 1: return launch_wino_kc<1>(a, g.threads, g.lds, grid, s);
-    case 2: return launch_wino_kc<2>(a, g.threads, g.lds, grid, s);
-    case 3: return launch_wino_kc<3>(a, g.threads, g.lds, grid, s);
-    default: return hipErrorInvalidValue;
-  }
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(g.threads), g.lds, s, a, sc);
+  return hipGetLastError();
 }
 
 int direct_g8(int M) {
@@ -478,6 +766,8 @@ int direct_g8(int M) {
 
 hipError_t launch_direct(DirectArgs a, hipStream_t s) {
   a.g8 = direct_g8(a.M);
+  a.Hp = (int32_t)padded_rows(a.H);
+  a.Wp = (int32_t)padded_cols(a.W);
   if (a.g8 > 256) return hipErrorInvalidValue;
   const int threads = 256;
   const int ppb = threads / a.g8;
@@ -486,7 +776,37 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
   const int64_t cap = (int64_t)cu_count() * 8;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(direct_conv_c1, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+  const bool fast = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && (a.M % 8) == 0 &&
+                    !a.epi.do_clip;
+  if (fast)
+    hipLaunchKernelGGL(direct_conv_c1<true>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+  else
+    hipLaunchKernelGGL(direct_conv_c1<false>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_eltwise(EltArgs a, bool binary, hipStream_t s) {
+  const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  hipLaunchKernelGGL(eltwise_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a,
+                     binary ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_dts(DtsArgs a, hipStream_t s) {
+  const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  hipLaunchKernelGGL(dts_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_input_convert(IoArgs a, hipStream_t s) {
+  const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  hipLaunchKernelGGL(input_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_output_convert(IoArgs a, hipStream_t s) {
+  const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  hipLaunchKernelGGL(output_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -1,4 +1,5 @@
-// Host launchers for the gfx950 kernels (defined in kernels.hip).
+// Host launchers for the gfx950 kernels (defined in kernels.hip). All launch
+// on the given stream and return the launch status.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -13,5 +14,9 @@ int winograd_max_m();   // output channels
 
 hipError_t launch_winograd(WinoArgs a, hipStream_t s);
 hipError_t launch_direct(DirectArgs a, hipStream_t s);
+hipError_t launch_eltwise(EltArgs a, bool binary, hipStream_t s);
+hipError_t launch_dts(DtsArgs a, hipStream_t s);
+hipError_t launch_input_convert(IoArgs a, hipStream_t s);
+hipError_t launch_output_convert(IoArgs a, hipStream_t s);
 
 }  // namespace arthip

@@ -34,7 +34,9 @@ extern "C" {
 typedef struct arthip_engine arthip_engine;
 
 /* Creates an engine bound to device_id (HipEngine::HipEngine,
- * hip_engine.h:90). Fails (1) when the device cannot be selected. */
+ * hip_engine.h:90). No device work happens here or in build: the device is
+ * selected and the stream created on the first run, which reports an invalid
+ * device. */
 int arthip_engine_create(int device_id, arthip_engine** out, char* err, int errlen);
 
 void arthip_engine_destroy(arthip_engine* eng);
@@ -72,6 +74,17 @@ int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64
 
 /* Human-readable plan of the last built shape (op list, fusions, buffers). */
 int arthip_engine_describe(const arthip_engine* eng, char* buf, int buflen);
+
+/* Per-launch GPU timing (the reference's VSHIP_PROFILE per-op events,
+ * hip_engine.cc:1409-1606): with profiling on, every launch of a run is
+ * bracketed by HIP events on the launch stream. profile_read synchronizes
+ * them and reports, per plan step, the summed milliseconds and launch count
+ * since the previous read (arrays of max_steps; step names newline-separated
+ * in names). Returns the number of plan steps, or a negative code. */
+int arthip_engine_set_profiling(arthip_engine* eng, int on);
+int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_ms,
+                               int64_t* launches, char* names, int names_len, char* err,
+                               int errlen);
 
 /* ------------------------------------------------------------------------ */
 /* Test-driver ABI: same names, arguments and return codes as the reference's */
@@ -113,10 +126,16 @@ size_t arthip_conv3x3_bias_len(int M);
 int arthip_conv3x3_pack(const uint16_t* w_oihw, const uint16_t* bias, int M, int C,
                         uint16_t* packed, size_t packed_cap, float* bias_out, size_t bias_cap);
 
-/* out = clip(skip1 + skip0 + act(conv3x3(in) + bias)) on NHWC fp16 device
- * buffers [N][H][W][C] -> [N][H][W][M]; SAME padding, stride 1. act: 0 none,
- * 1 ReLU, 2 SiLU. skip0/skip1: NHWC [N][H][W][M] or NULL. The fused form of
- * the reference's winograd_conv / direct_conv launches
+/* Internal activation layout used by the kernel-level entry points: NHWC fp16
+ * with a zero border, [N][Hp][Wp][C] with Hp = 2*ceil(H/2) + 2 and
+ * Wp = 2*ceil(W/2) + 2; pixel (h, w) lives at row h + 1, column w + 1. The
+ * border must be zero (allocate zero-filled) and is never written. */
+int arthip_padded_dims(int H, int W, int* Hp, int* Wp);
+
+/* out = skip1 + skip0 + act(conv3x3(in) + bias) on padded NHWC fp16 device
+ * buffers ([N][Hp][Wp][C] -> [N][Hp][Wp][M]); SAME padding, stride 1. act: 0
+ * none, 1 ReLU, 2 SiLU. skip0/skip1: padded [N][Hp][Wp][M] or NULL. The fused
+ * form of the reference's winograd_conv / direct_conv launches
  * (src/common/hip_kernels.h:143-483). stream may be NULL. */
 int arthip_conv3x3_f16_nhwc(const void* in, const void* packed, const float* bias, int act,
                             const void* skip0, const void* skip1, void* out, int N, int H, int W,

@@ -42,3 +42,15 @@ def pytest_collection_modifyitems(config, items):
 @pytest.fixture(scope="session")
 def device() -> int:
     return int(os.environ.get("ARTHIP_TEST_DEVICE", "0"))
+
+
+@pytest.fixture(scope="session")
+def fixtures(tmp_path_factory):
+    from tests.fixtures import FixtureSet
+    return FixtureSet(tmp_path_factory.mktemp("fixtures"))
+
+
+@pytest.fixture(scope="session")
+def harness():
+    from arthip_amd.engine import EngineHarness
+    return EngineHarness()
