@@ -1,0 +1,106 @@
+"""The C ABI: every function include/arthip.h declares is exported by the built
+library, the host fp16 conversion is IEEE round-to-nearest-even, and the host
+filter transform packs U' = 4 * G g G^T in the documented MFMA operand order.
+All CPU-only (no compute call touches a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+
+from arthip_amd import _lib
+from oracle import ops as orc
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "arthip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b([a-z_][a-z0-9_]*)\s*\(", text)) - {"sizeof"})
+
+
+def test_header_declares_expected_surface():
+    names = declared_functions()
+    for n in ("engine_probe", "engine_run", "engine_alloc_failure_then_run",
+              "arthip_engine_run_device", "arthip_conv3x3_f16_nhwc"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(declared_functions()) == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_host_fp16_conversion_is_rne():
+    lib = _lib.lib()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    h = np.unique(h[np.isfinite(h)].astype(np.float64))
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32)
+    xs = np.concatenate([h.astype(np.float32), mids, np.nextafter(mids, np.float32(np.inf)),
+                         np.array([65520, 1e9, 2.0 ** -25, 3e-8], np.float32)])
+    got = np.array([lib.arthip_f32_to_f16(float(v)) for v in xs], np.uint16)
+    np.testing.assert_array_equal(got, xs.astype(np.float16).view(np.uint16))
+    back = np.array([lib.arthip_f16_to_f32(int(b)) for b in range(0, 65536, 7)], np.float32)
+    want = np.arange(0, 65536, 7, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(back[np.isfinite(want)], want[np.isfinite(want)])
+
+
+def test_winograd_pack_layout():
+    """U'[ob][p][kc][lane][e] = fp16(4 * U_p[m][c]) with m = 16*ob + lane % 16 and
+    c = 32*kc + 8*(lane // 16) + e (v_mfma_f32_16x16x32_f16 A-operand order)."""
+    lib = _lib.lib()
+    rng = np.random.default_rng(5)
+    for c_in, m_out in [(64, 64), (4, 8), (40, 20), (96, 96)]:
+        w = (rng.standard_normal((m_out, c_in, 3, 3)) * 0.2).astype(np.float16)
+        n_u = lib.arthip_conv3x3_packed_halfs(m_out, c_in)
+        n_b = lib.arthip_conv3x3_bias_len(m_out)
+        u = np.zeros(n_u, np.uint16)
+        b = np.zeros(n_b, np.float32)
+        bias = rng.standard_normal(m_out).astype(np.float16)
+        rc = lib.arthip_conv3x3_pack(
+            w.view(np.uint16).ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+            bias.view(np.uint16).ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), m_out, c_in,
+            u.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n_u,
+            b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n_b)
+        assert rc == 0
+        kc = (c_in + 31) // 32
+        n_ob = (m_out + 15) // 16
+        up = u.view(np.float16).reshape(n_ob, 16, kc, 64, 8).astype(np.float64)
+        for m in range(m_out):
+            for c in range(c_in):
+                want = (4.0 * orc.winograd_filter(w[m, c].astype(np.float64))).astype(np.float16)
+                ob, row = divmod(m, 16)
+                k, kk = divmod(c, 32)
+                lane, e = row + 16 * (kk // 8), kk % 8
+                np.testing.assert_array_equal(up[ob, :, k, lane, e], want.reshape(16).astype(np.float64))
+        # padding is zero
+        mask = np.ones_like(up, bool)
+        for m in range(m_out):
+            for c in range(c_in):
+                ob, row = divmod(m, 16)
+                k, kk = divmod(c, 32)
+                mask[ob, :, k, row + 16 * (kk // 8), kk % 8] = False
+        assert not up[mask].any()
+        np.testing.assert_array_equal(b[:m_out], bias.astype(np.float32))
+        assert not b[m_out:].any()
+
+
+def test_padded_dims():
+    lib = _lib.lib()
+    hp, wp = ctypes.c_int(), ctypes.c_int()
+    for h, w in [(1080, 1920), (1, 1), (17, 33)]:
+        assert lib.arthip_padded_dims(h, w, ctypes.byref(hp), ctypes.byref(wp)) == 0
+        assert hp.value == 2 * ((h + 1) // 2) + 2 and wp.value == 2 * ((w + 1) // 2) + 2
+
+
+def test_bench_refuses_several_gpus():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(HEADER.parents[1] / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "one GPU" in r.stderr

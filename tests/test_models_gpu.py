@@ -93,3 +93,68 @@ def test_fresh_engines_bit_identical():
             first = out
         else:
             np.testing.assert_array_equal(out, first)
+
+
+def _band_check(got_full, spec, x, r0, r1, margin):
+    """Oracle on input rows [r0-margin, r1+margin) (full width); compares output rows
+    for input rows [r0, r1), which do not see the band's artificial edges."""
+    band = np.ascontiguousarray(x[:, :, r0 - margin:r1 + margin, :])
+    want = run_model(spec.model, band)
+    s = spec.scale
+    want = want[:, :, margin * s:(margin + r1 - r0) * s, :]
+    got = got_full[:, :, r0 * s:r1 * s, :]
+    exact = run_model(spec.model, band, round_fp16=False)[:, :, margin * s:(margin + r1 - r0) * s, :]
+    return _compare(got, want), _compare(want, exact)
+
+
+def test_r8f64_full_1080p_band_parity():
+    """Full-size frame on the GPU; the oracle checks a 32-row band in the middle
+    (receptive field of 18 3x3 convs = 18 rows of margin)."""
+    spec = models.r8f64(seed=0)
+    x = models.synthetic_input((1, 1, 1080, 1920), seed=1)
+    with Engine(0) as e:
+        got = e.build(spec).run(x).astype(np.float32)
+        again = e.run(x)
+    np.testing.assert_array_equal(got, again.astype(np.float32))
+    assert got.shape == (1, 1, 2160, 3840) and np.isfinite(got).all()
+    s, floor = _band_check(got, spec, x, 520, 552, 18)
+    print("r8f64 1080p band", s, "floor", floor)
+    assert s["rel_rms"] <= max(4 * floor["rel_rms"], 2e-3), (s, floor)
+
+
+def test_r8f64_4k_batch2_full_size():
+    """BASELINE's 4K x2 config at full size: finite, each image equal to its own
+    single-image run, and band parity against the oracle."""
+    spec = models.r8f64(seed=0)
+    x = models.synthetic_input((2, 1, 2160, 3840), seed=5)
+    with Engine(0) as e:
+        e.build(spec)
+        got = e.run(x)
+        one = e.run(np.ascontiguousarray(x[1:2]))
+    assert got.shape == (2, 1, 4320, 7680) and np.isfinite(got).all()
+    np.testing.assert_array_equal(got[1:2], one)
+    s, floor = _band_check(got[1:2].astype(np.float32), spec, x[1:2], 1000, 1016, 18)
+    print("r8f64 4k band", s, "floor", floor)
+    assert s["rel_rms"] <= max(4 * floor["rel_rms"], 2e-3), (s, floor)
+
+
+def test_shipped_model_on_real_image_meets_gate():
+    """The reference's shipped luma model on its own 256x256 test image (BT.601
+    luma): bounded [0,1] output, so the literal gate applies."""
+    from pathlib import Path
+
+    from PIL import Image
+
+    from arthip_amd import onnx_proto as op
+    here = Path(__file__).resolve().parent / "golden"
+    rgb = np.asarray(Image.open(here / "test_256.png").convert("RGB"), np.float32) / 255.0
+    y = (rgb[..., 0] * 0.299 + rgb[..., 1] * 0.587 + rgb[..., 2] * 0.114)[None, None]
+    x = y.astype(np.float16)
+    model = op.load(here / "ArtCNN_R8F64_fp16.onnx")
+    with Engine(0) as e:
+        got = e.build(model).run(x).astype(np.float32)
+    want = run_model(model, x)
+    s = _compare(got, want)
+    print("shipped luma 256x256", s)
+    assert got.shape == (1, 1, 512, 512)
+    assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
