@@ -48,7 +48,24 @@ def parse():
                    help="rows of the frame in the CPU baseline sample (0 disables it)")
     p.add_argument("--no-profile", action="store_true",
                    help="skip the per-launch event timing (roofline becomes null)")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                   help="instead of the bench, run a plain device copy of MB megabytes "
+                        "(--steps times): the known-traffic kernel that scales rocprofv3 "
+                        "FETCH_SIZE / WRITE_SIZE readings")
     return p.parse_args()
+
+
+def calibrate_copy(mb: int, steps: int) -> int:
+    import torch
+    n = mb * (1 << 20) // 2
+    x = torch.ones(n, dtype=torch.float16, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(steps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes_read": 2 * n, "calibrate_copy_bytes_written": 2 * n,
+                      "launches": steps}), flush=True)
+    return 0
 
 
 def cpu_baseline(spec, x_full, rows: int) -> dict | None:
@@ -90,9 +107,12 @@ def traffic_from_profiles(kernel_key: str):
 
 def main() -> int:
     args = parse()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy, args.steps)
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by frame or by H-band, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: measures one GPU only; --gpus {args.gpus} is not supported "
+              "(frames are independent: several GPUs would each run whole frames)",
+              file=sys.stderr)
         return 2
 
     import numpy as np

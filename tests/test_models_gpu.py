@@ -2,7 +2,7 @@
 
 The oracle (oracle/model.py) evaluates the same ONNX model node by node in fp32
 with fp16 tensors between nodes -- ONNX Runtime CPU EP semantics for an fp16
-model. Gates (BASELINE north star): max-abs <= 2e-2 and PSNR >= 50 dB (peak 1)
+model. Gates: max-abs <= 2e-2 and PSNR >= 50 dB (peak 1)
 where the configuration's output range allows it (C4F32, the single layer);
 for the deep He-normal models the fp16-storage floor of the model itself is
 far above that (outputs span ~+-200), so those are gated on relative RMS error
@@ -123,7 +123,7 @@ def test_r8f64_full_1080p_band_parity():
 
 
 def test_r8f64_4k_batch2_full_size():
-    """BASELINE's 4K x2 config at full size: finite, each image equal to its own
+    """R8F64 on a batch of two 3840x2160 frames at full size: finite, each image equal to its own
     single-image run, and band parity against the oracle."""
     spec = models.r8f64(seed=0)
     x = models.synthetic_input((2, 1, 2160, 3840), seed=5)

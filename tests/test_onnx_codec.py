@@ -45,7 +45,7 @@ def test_roundtrip_preserves_fields():
 def test_decodes_shipped_model():
     m = op.load(SHIPPED)
     c = collections.Counter(n.op_type for n in m.graph.nodes)
-    # SURVEY-decoded structure of the shipped luma model: 70 nodes.
+    # Structure of the shipped luma model: 70 nodes.
     assert len(m.graph.nodes) == 70
     assert c == {"Conv": 27, "Sigmoid": 16, "Mul": 16, "Add": 9, "DepthToSpace": 1, "Clip": 1}
     assert m.graph.inputs[0].elem_type == op.FLOAT16
