@@ -270,6 +270,7 @@ __device__ __forceinline__ void item_coords(const WinoSched& sc, int sb, int nti
 //        prefetched into registers while the current item runs on MFMA.
 template <int KC, bool CVEC, bool FAST, bool PF>
 __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
+  constexpr bool SKIP_PF = false;
   extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
   constexpr int CP = KC * 32;  // padded input channels
   constexpr int TS = CP + 8;   // LDS halfs per tile row (16-byte pad)
@@ -339,9 +340,10 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
     const bool h1 = oh + 1 < a.H, w1 = ow + 1 < a.W;
     const int64_t ppix = ((int64_t)n * a.Hp + oh + 1) * a.Wp + ow + 1;
     const int64_t prow = (int64_t)a.Wp * a.M;
-    // Residual inputs for the fast epilogue, requested before the MFMA work.
+    // Residual inputs for the fast epilogue. SKIP_PF requests them before the
+    // MFMA work (16 more live VGPRs); otherwise they load in the epilogue.
     h4 sk[2][4];
-    if (FAST) {
+    auto load_skips = [&]() {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const _Float16* sp = reinterpret_cast<const _Float16*>(s == 0 ? a.epi.skip0 : a.epi.skip1);
@@ -357,7 +359,8 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
           }
         }
       }
-    }
+    };
+    if (FAST && SKIP_PF) load_skips();
 
     // ---- 16 position GEMMs on MFMA, folded row by row into the 2x2 tile
     f4 y[4];
@@ -403,6 +406,7 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
     }
 
     // ---- epilogue: lane holds 4 channels x the 4 pixels of one tile
+    if (FAST && !SKIP_PF) load_skips();
     if (valid) {
       if (FAST) {
         _Float16* o = reinterpret_cast<_Float16*>(a.epi.out) + ppix * a.M + ch0;
@@ -738,7 +742,11 @@ hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
   const bool cvec = (a.C % 4) == 0;
   const bool fast = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && (a.M % 4) == 0 &&
                     !a.epi.do_clip;
-  const bool pf = 16 * g.tb * g.kc * 8 == g.threads;  // one input task per thread
+  // Register prefetch of the next item's patch costs 32 VGPRs; on top of the
+  // 128-VGPR U' slice (C = 64) that spills to scratch, and every reload then
+  // waits on all outstanding memory traffic. Measured on R8F64 1080p: 373 us per
+  // 64->64 ReLU layer with the prefetch vs 218 us without, so it stays off.
+  const bool pf = false;
   WinoKernel fn = wino_kernel(g.kc, cvec, fast, pf);
   if (fn == nullptr) return hipErrorInvalidValue;
   if (g.lds > 65536) {
