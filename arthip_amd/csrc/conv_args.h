@@ -61,6 +61,29 @@ struct WinoArgs {
   int32_t n_sb;              // total work items = N * tiles_h * sb_w
 };
 
+// Invariant-divisor division x / d = (((x * m) >> 32) + x) >> s for uniform
+// divisors (valid for x < 2^31); built on the host by make_fastdiv.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+// Winograd F(2x2,3x3) conv with C == M in {32, 64} and the fast epilogue
+// (winograd_strip in kernels.hip). Work items are 1 tile row x 16 tile columns,
+// ordered (n, strip of 16 tile columns, tile row) with the tile row fastest, so
+// consecutive items of a workgroup slide down one strip.
+struct StripArgs {
+  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C]
+  const uint16_t* u;   // packed transformed filters (winograd_pack)
+  const float* bias;   // [C] fp32
+  const uint16_t* skip0;
+  const uint16_t* skip1;
+  uint16_t* out;  // padded NHWC fp16, same geometry as the input
+  int32_t N, H, W, Hp, Wp;
+  int32_t tiles_h, tiles_w, n_strips;
+  int32_t n_items;  // N * n_strips * tiles_h
+  FastDiv fd_tiles_h, fd_strips;
+};
+
 // Direct 3x3 conv for a single input channel (the model's head conv).
 struct DirectArgs {
   const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][1]

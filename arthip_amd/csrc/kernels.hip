@@ -70,10 +70,6 @@ __device__ __forceinline__ h4 to_h4(f4 v) {
 
 // Invariant-divisor division for the persistent work-item index (uniform
 // values; avoids the long scalar division sequence). Valid for x < 2^31.
-struct FastDiv {
-  uint32_t d, m, s;
-};
-
 __device__ __forceinline__ uint32_t fdiv(uint32_t x, FastDiv f) {
   const uint64_t t = (static_cast<uint64_t>(x) * f.m) >> 32;
   return static_cast<uint32_t>((t + x) >> f.s);
@@ -443,6 +439,287 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
 }
 
 // ---------------------------------------------------------------------------
+// Winograd F(2x2,3x3), sliding-window variant for C == M in {32, 64}
+// ---------------------------------------------------------------------------
+//
+// A workgroup of 2*KC waves (one 16-wide output-channel block each) walks a
+// contiguous range of work items, each 1 tile row x 16 tile columns, ordered
+// down a 16-tile-wide strip. Consecutive items of a strip share two of their
+// four input rows, so a thread keeps the lower two rows of its 4x4 patch in
+// registers and loads only the two new rows; the loads are issued right after
+// the item's barrier and land while the item runs on the matrix cores. V' is
+// double-buffered in LDS, so one barrier per item suffices: a wave writing
+// buffer b for item i+2 has passed the barrier of item i+1, which every wave
+// reaches only after its MFMA reads of item i.
+//
+// Fold: with m_rc the product at position (r, c) (column 3 negated by the
+// input transform), row r needs P_r = m_r0 + m_r1 + m_r2 and
+// Q_r = m_r1 - m_r2 + m_r3. Chaining the accumulators gives
+// X = m_r2, b = X + m_r1, P_r = b + m_r0, c = b + m_r3 and Q_r = c - 2X with
+// one fused multiply-add per value. Row 1 starts from the bias instead
+// (Y = bias + m_11; b = Y + m_12; P_1 = b + m_10; c = Y + m_13; Q_1 = c - b + Y):
+// (1,1) is the one position every output takes with coefficient +1, so the
+// bias lands exactly once in each output. Then
+//   y00 = P0 + P1 + P2, y01 = Q0 + Q1 + Q2, y10 = P1 - P2 - P3, y11 = Q1 - Q2 - Q3.
+
+// V' of one input task (4 channels x one tile) into the V' buffer; same
+// transform and scaling as store_v, with the patch rows split in two halves.
+// The patch is held as half2 pairs (element 2*(4*row + col) + e, channel pair
+// e) so that loop-carried values stay in the packed form the v_pk_* ops use.
+// a - b on a half2 pair in one packed add. Written as a plain subtraction in
+// strip_transform, the compiler splits this one into two half-precision
+// subtractions and a pack (three instructions instead of one).
+__device__ __forceinline__ h2 pk_sub(h2 a, h2 b) {
+  h2 r;
+  asm("v_pk_add_f16 %0, %1, %2 neg_lo:[0,1] neg_hi:[0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+template <int KC>
+__device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16],
+                                                const h2 (&bot)[16]) {
+  constexpr int WPS = 16 * (32 * KC + 8);
+  const h2 qp = {0.25f16, 0.25f16};
+  const h2 qn = {-0.25f16, -0.25f16};
+  h2 t[4][4][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const h2 d0 = top[2 * j + e], d1 = top[2 * (4 + j) + e];
+      const h2 d2 = bot[2 * j + e], d3 = bot[2 * (4 + j) + e];
+      t[0][j][e] = pk_sub(d0, d2);
+      t[1][j][e] = d1 + d2;
+      t[2][j][e] = d2 - d1;
+      t[3][j][e] = d1 - d3;
+    }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h2 o[4][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const h2 n1 = t[i][1][e] * qn;
+      const h2 n2 = t[i][2][e] * qn;
+      o[0][e] = __builtin_elementwise_fma(t[i][0][e], qp, n2);
+      o[1][e] = __builtin_elementwise_fma(t[i][1][e], qp, -n2);
+      o[2][e] = __builtin_elementwise_fma(t[i][2][e], qp, n1);
+      o[3][e] = __builtin_elementwise_fma(t[i][3][e], qp, n1);
+    }
+    _Float16* row = vw + (4 * i) * WPS;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      *reinterpret_cast<h4*>(row + k * WPS) = __builtin_shufflevector(o[k][0], o[k][1], 0, 1, 2, 3);
+  }
+}
+
+// Fast epilogue of 4 channels whose accumulator already holds the bias.
+template <int ACT>
+__device__ __forceinline__ h4 strip_epi4(f4 y, h4 s0, h4 s1) {
+  h4 r = to_h4(y);
+  if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
+  if (ACT == kActSilu) {
+    f4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = (float)r[e];
+      t[e] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    }
+    r = to_h4(t);
+  }
+  r += s0;
+  r += s1;
+  return r;
+}
+
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+
+// Two waves per SIMD: at most 256 registers per lane (U' takes 64 * KC).
+template <int KC, int ACT, int NSKIP>
+__global__ void __launch_bounds__(128 * KC) __attribute__((amdgpu_waves_per_eu(2, 2)))
+winograd_strip(StripArgs a) {
+  constexpr int C = 32 * KC;   // input channels = output channels
+  constexpr int TS = C + 8;    // LDS halfs per tile row (16-byte pad)
+  constexpr int WPS = 16 * TS; // halfs per position
+  constexpr int VBUF = 16 * WPS;
+  constexpr int QUADS = C / 4;
+  constexpr int PX = 2 * C;    // bytes per pixel
+  extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+
+  // Contiguous item range; workgroup id % 8 is the XCD, and each XCD takes a
+  // contiguous eighth of the items.
+  const int G = gridDim.x;
+  const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int begin = (int)((int64_t)a.n_items * slot / G);
+  const int end = (int)((int64_t)a.n_items * (slot + 1) / G);
+  if (begin >= end) return;  // uniform across the workgroup
+
+  h8 u[16][KC];
+  {
+    const h8* up = reinterpret_cast<const h8*>(a.u) + (size_t)wave * (16 * KC * 64) + lane;
+#pragma unroll
+    for (int p = 0; p < 16; ++p)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) u[p][kc] = up[(p * KC + kc) * 64];
+  }
+
+  // Input task: tile tt of the item, channels [4*tq, 4*tq + 4).
+  const int tt = tid / QUADS;
+  const int tq = tid - tt * QUADS;
+  // MFMA / epilogue lane: tile tcol; B rows 8*kq.. of each 32-channel chunk;
+  // output channels [ch0, ch0 + 4).
+  const int tcol = lane & 15;
+  const int kq = lane >> 4;
+  const int ch0 = 16 * wave + 4 * kq;
+  const f4 bias4 = *reinterpret_cast<const f4*>(a.bias + ch0);
+  _Float16* const vw0 = vlds + tt * TS + 4 * tq;
+  _Float16* const vw1 = vw0 + VBUF;
+  const _Float16* const vr0 = vlds + tcol * TS + 8 * kq;
+  const _Float16* const vr1 = vr0 + VBUF;
+  const uint32_t out_lane = (uint32_t)(2 * tcol * C + ch0) * 2;
+  const int64_t row_bytes = (int64_t)a.Wp * PX;
+
+  int n, s, th;
+  auto decode = [&](int item) {
+    const uint32_t sg = fdiv((uint32_t)item, a.fd_tiles_h);
+    th = item - (int)(sg * (uint32_t)a.tiles_h);
+    const uint32_t nn = fdiv(sg, a.fd_strips);
+    s = (int)(sg - nn * (uint32_t)a.n_strips);
+    n = (int)nn;
+  };
+  // Byte offset of this thread's patch within a strip row; tiles past the
+  // right edge read tile 0's patch (their outputs are never stored).
+  uint32_t in_lane = 0;
+  auto in_row = [&](int r) {
+    return reinterpret_cast<const char*>(a.in) + (((int64_t)n * a.Hp + r) * a.Wp + 32 * s) * PX;
+  };
+  auto load2 = [&](h2 (&x)[16], const char* rb) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h4 v = *reinterpret_cast<const h4*>(rb + r * row_bytes + in_lane + j * PX);
+        x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
+        x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
+      }
+  };
+
+  // One item: transform, barrier, loads for the next item of the strip, MFMA
+  // and epilogue. The next item's two new rows go into `top` (the rows the
+  // transform just consumed); past the last item of the run the row index is
+  // clamped to the last two rows of the padded image, which are loaded and
+  // never used, so the loop body has no data-dependent branch around a load.
+  h2 A[16], B[16];
+  auto body = [&](auto buf_tag, h2 (&top)[16], h2 (&bot)[16]) {
+    constexpr int BUF = decltype(buf_tag)::value;
+    _Float16* const vw = BUF ? vw1 : vw0;
+    const _Float16* const vr = BUF ? vr1 : vr0;
+    strip_transform<KC>(vw, top, bot);
+    lds_sync();
+
+    const bool vt = 16 * s + tcol < a.tiles_w;
+    const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + 32 * s + 1;
+    // Residual inputs of this item (in-bounds for every valid tile: the pixel
+    // right of / below the tile is at worst the zero border).
+    h4 sk[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sk[k][q] = h4{0, 0, 0, 0};
+    if (NSKIP > 0 && vt) {
+#pragma unroll
+      for (int k = 0; k < NSKIP; ++k) {
+        const char* sb = reinterpret_cast<const char*>(k == 0 ? a.skip0 : a.skip1) + pix0 * PX;
+        sk[k][0] = *reinterpret_cast<const h4*>(sb + out_lane);
+        sk[k][1] = *reinterpret_cast<const h4*>(sb + out_lane + PX);
+        sk[k][2] = *reinterpret_cast<const h4*>(sb + row_bytes + out_lane);
+        sk[k][3] = *reinterpret_cast<const h4*>(sb + row_bytes + out_lane + PX);
+      }
+    }
+    {
+      const int r = 2 * th + 4;
+      load2(top, in_row(r < a.Hp - 2 ? r : a.Hp - 2));
+    }
+
+    // 16 position GEMMs, folded through the accumulator chains.
+    auto mm = [&](int p, f4 acc) {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            u[p][kc], *reinterpret_cast<const h8*>(vr + p * WPS + kc * 32), acc, 0, 0, 0);
+      return acc;
+    };
+    const f4 z = {0, 0, 0, 0};
+    const f4 m2 = {-2.0f, -2.0f, -2.0f, -2.0f};
+    f4 P[4], Q[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (r == 1) {
+        const f4 Y = mm(5, bias4);
+        const f4 b = mm(6, Y);
+        P[1] = mm(4, b);
+        const f4 c = mm(7, Y);
+        Q[1] = (c - b) + Y;
+      } else {
+        const f4 X = mm(4 * r + 2, z);
+        const f4 b = mm(4 * r + 1, X);
+        P[r] = mm(4 * r, b);
+        const f4 c = mm(4 * r + 3, b);
+        Q[r] = __builtin_elementwise_fma(X, m2, c);
+      }
+    }
+    const f4 y00 = (P[0] + P[1]) + P[2];
+    const f4 y01 = (Q[0] + Q[1]) + Q[2];
+    const f4 y10 = (P[1] - P[2]) - P[3];
+    const f4 y11 = (Q[1] - Q[2]) - Q[3];
+
+    if (vt) {
+      const bool w1 = 2 * (16 * s + tcol) + 1 < a.W;
+      const bool h1 = 2 * th + 1 < a.H;
+      char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
+      *reinterpret_cast<h4*>(ob + out_lane) = strip_epi4<ACT>(y00, sk[0][0], sk[1][0]);
+      if (w1)
+        *reinterpret_cast<h4*>(ob + out_lane + PX) = strip_epi4<ACT>(y01, sk[0][1], sk[1][1]);
+      if (h1) {
+        *reinterpret_cast<h4*>(ob + row_bytes + out_lane) =
+            strip_epi4<ACT>(y10, sk[0][2], sk[1][2]);
+        if (w1)
+          *reinterpret_cast<h4*>(ob + row_bytes + out_lane + PX) =
+              strip_epi4<ACT>(y11, sk[0][3], sk[1][3]);
+      }
+    }
+    ++th;
+  };
+
+  // Runs: maximal stretches of the item range within one strip.
+  for (int it = begin; it < end;) {
+    decode(it);
+    const int len = min(end - it, a.tiles_h - th);
+    {
+      const int t = (16 * s + tt < a.tiles_w) ? tt : 0;
+      in_lane = (uint32_t)(2 * t * C + 4 * tq) * 2;
+    }
+    load2(A, in_row(2 * th));
+    load2(B, in_row(2 * th + 2));
+    // The buffer parity restarts with each run; this barrier keeps the first
+    // transform of the run behind every wave's last MFMA reads.
+    lds_sync();
+    for (int k = len;;) {
+      body(IntC<0>{}, A, B);
+      if (--k == 0) break;
+      body(IntC<1>{}, B, A);
+      if (--k == 0) break;
+    }
+    it += len;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Direct 3x3 conv with one input channel (head conv)
 // ---------------------------------------------------------------------------
 
@@ -728,7 +1005,85 @@ WinoGeom winograd_geom(int C, int M) {
 int winograd_max_kc() { return 3; }
 int winograd_max_m() { return 128; }
 
+namespace {
+
+using StripKernel = void (*)(StripArgs);
+
+template <int KC, int ACT>
+StripKernel strip_kernel_skips(int nskip) {
+  switch (nskip) {
+    case 0: return winograd_strip<KC, ACT, 0>;
+    case 1: return winograd_strip<KC, ACT, 1>;
+    case 2: return winograd_strip<KC, ACT, 2>;
+    default: return nullptr;
+  }
+}
+
+template <int KC>
+StripKernel strip_kernel_act(int act, int nskip) {
+  switch (act) {
+    case kActNone: return strip_kernel_skips<KC, kActNone>(nskip);
+    case kActRelu: return strip_kernel_skips<KC, kActRelu>(nskip);
+    case kActSilu: return strip_kernel_skips<KC, kActSilu>(nskip);
+    default: return nullptr;
+  }
+}
+
+// winograd_strip covers C == M in {32, 64} with the fast epilogue.
+bool strip_eligible(const WinoArgs& a) {
+  return a.C == a.M && (a.C == 32 || a.C == 64) && a.epi.out_kind == kOutPadded &&
+         a.epi.dts_b < 2 && !a.epi.do_clip &&
+         (a.epi.act == kActNone || a.epi.act == kActRelu || a.epi.act == kActSilu);
+}
+
+hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
+  StripArgs a{};
+  a.in = w.in;
+  a.u = w.u;
+  a.bias = w.epi.bias;
+  a.skip0 = w.epi.skip0 ? w.epi.skip0 : w.epi.skip1;
+  a.skip1 = w.epi.skip0 ? w.epi.skip1 : nullptr;
+  const int nskip = (a.skip0 != nullptr) + (a.skip1 != nullptr);
+  a.out = reinterpret_cast<uint16_t*>(w.epi.out);
+  a.N = w.N;
+  a.H = w.H;
+  a.W = w.W;
+  a.Hp = (int32_t)padded_rows(w.H);
+  a.Wp = (int32_t)padded_cols(w.W);
+  a.tiles_h = (w.H + 1) / 2;
+  a.tiles_w = (w.W + 1) / 2;
+  a.n_strips = (a.tiles_w + 15) / 16;
+  const int64_t items = (int64_t)a.N * a.n_strips * a.tiles_h;
+  if (items >= (int64_t)1 << 31) return hipErrorInvalidValue;
+  a.n_items = (int32_t)items;
+  a.fd_tiles_h = make_fastdiv((uint32_t)a.tiles_h);
+  a.fd_strips = make_fastdiv((uint32_t)a.n_strips);
+  const int kc = w.C / 32;
+  StripKernel fn = kc == 1 ? strip_kernel_act<1>(w.epi.act, nskip)
+                           : strip_kernel_act<2>(w.epi.act, nskip);
+  if (fn == nullptr) return hipErrorInvalidValue;
+  const int threads = 128 * kc;
+  const size_t lds = (size_t)2 * 16 * 16 * (32 * kc + 8) * 2;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, lds) != hipSuccess ||
+      occ < 1)
+    occ = 1;
+  int64_t grid = (int64_t)cu_count() * occ;
+  if (grid > items) grid = items;
+  grid = (grid + 7) / 8 * 8;
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(threads), lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
+  if (strip_eligible(a)) return launch_strip(a, s);
   const WinoGeom g = winograd_geom(a.C, a.M);
   a.n_ob = g.n_ob;
   a.tb = g.tb;

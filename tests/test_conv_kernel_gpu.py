@@ -116,10 +116,13 @@ def check(got, ref, label):
     # up to 2^-11 |ref| each (two ulps in all: the engine and the oracle may round
     # a conv value to neighbouring fp16 values); fp16 U and V (F(2x2,3x3)
     # Winograd) add roundings of the per-position partial products, which scale
-    # with the typical term size, not with each output. A wrong index or a dropped
-    # term produces errors of the order of rms(ref).
+    # with the typical term size, not with each output: an fp16 emulation of the
+    # transform arithmetic on 64 channels puts the 0.99999 quantile of
+    # |err| / rms(ref) at 3.9e-3, so over the 15M outputs of the largest case the
+    # tail reaches about 5e-3. A wrong index or a dropped term produces errors of
+    # the order of rms(ref).
     rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2))) + 1e-30
-    tol = 2.0 ** -9 * np.abs(ref) + 4e-3 * rms
+    tol = 2.0 ** -9 * np.abs(ref) + 6e-3 * rms
     bad = err > tol
     rel_rms = float(np.sqrt(np.mean((got - ref).astype(np.float64) ** 2))) / rms
     assert not bad.any(), (f"{label}: {bad.sum()} elements off, max err {err.max():.4g} "
@@ -167,3 +170,47 @@ def test_deterministic():
     a = run_conv(x, wt, b, 1)
     for _ in range(3):
         np.testing.assert_array_equal(a, run_conv(x, wt, b, 1))
+
+
+# C == M in {32, 64} with the fast epilogue runs the sliding-window kernel
+# (winograd_strip): work items slide down 16-tile-wide strips, so these cases
+# vary the strip count, partial right-edge strips, odd heights (the last tile
+# row stores one output row), batches and runs that cross strip boundaries.
+@pytest.mark.parametrize("h,w", GEOMETRY)
+def test_strip_geometry(h, w):
+    x, wt, b = make_case(8, 1, 64, 64, h, w)
+    rng = np.random.default_rng(9)
+    skips = [rng.standard_normal((1, 64, h, w)).astype(np.float16)]
+    check(run_conv(x, wt, b, 1, skips), oracle_conv(x, wt, b, 1, skips), f"strip64 {h}x{w}")
+
+
+@pytest.mark.parametrize("h,w", [(8, 8), (17, 33), (33, 17), (1082, 64), (54, 1920)])
+def test_strip_c32(h, w):
+    x, wt, b = make_case(10, 1, 32, 32, h, w)
+    rng = np.random.default_rng(11)
+    skips = [rng.standard_normal((1, 32, h, w)).astype(np.float16) for _ in range(2)]
+    check(run_conv(x, wt, b, 0, skips), oracle_conv(x, wt, b, 0, skips), f"strip32 {h}x{w}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("nskip", [0, 1, 2])
+def test_strip_epilogue_c32(act, nskip):
+    x, wt, b = make_case(12, 1, 32, 32, 19, 35)
+    rng = np.random.default_rng(13)
+    skips = [rng.standard_normal((1, 32, 19, 35)).astype(np.float16) for _ in range(nskip)]
+    check(run_conv(x, wt, b, act, skips), oracle_conv(x, wt, b, act, skips),
+          f"strip32 act{act} skip{nskip}")
+
+
+def test_strip_batch_odd():
+    x, wt, b = make_case(14, 3, 64, 64, 17, 45)
+    rng = np.random.default_rng(15)
+    skips = [rng.standard_normal((3, 64, 17, 45)).astype(np.float16) for _ in range(2)]
+    check(run_conv(x, wt, b, 2, skips), oracle_conv(x, wt, b, 2, skips), "strip batch3 17x45")
+
+
+def test_strip_long_runs():
+    # 180 tile rows x 20 strips: every workgroup walks several items of a strip
+    # and most ranges cross a strip boundary.
+    x, wt, b = make_case(16, 1, 64, 64, 360, 640)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), "strip 360x640")
