@@ -460,7 +460,8 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
 // (Y = bias + m_11; b = Y + m_12; P_1 = b + m_10; c = Y + m_13; Q_1 = c - b + Y):
 // (1,1) is the one position every output takes with coefficient +1, so the
 // bias lands exactly once in each output. Then
-//   y00 = P0 + P1 + P2, y01 = Q0 + Q1 + Q2, y10 = P1 - P2 - P3, y11 = Q1 - Q2 - Q3.
+//   y00 = P0 + P1 + P2, y01 = Q0 + Q1 + Q2, y10 = P1 - P2 - P3, y11 = Q1 - Q2 - Q3,
+// accumulated row by row.
 
 // V' of one input task (4 channels x one tile) into the V' buffer; same
 // transform and scaling as store_v, with the patch rows split in two halves.
@@ -475,10 +476,26 @@ __device__ __forceinline__ h2 pk_sub(h2 a, h2 b) {
   return r;
 }
 
+// V' tile-row length in halfs. C = 64 uses 128-byte rows with the eight
+// 16-byte channel groups of tile t stored at group index g ^ (t & 7): the MFMA
+// B reads (16 tiles x one group per lane) then run at about 160 B/clk per CU on
+// gfx950, against 112 B/clk with the padded 144-byte rows, which C = 32 keeps.
+template <int KC>
+struct StripLds {
+  static constexpr bool SWZ = KC == 2;
+  static constexpr int TS = SWZ ? 32 * KC : 32 * KC + 8;
+  static constexpr int WPS = 16 * TS;  // halfs per position
+  static constexpr int VBUF = 16 * WPS;
+  // Half offset of channel c (multiple of 4) of tile t within a position.
+  __host__ __device__ static constexpr int at(int t, int c) {
+    return t * TS + (SWZ ? (((c >> 3) ^ (t & 7)) << 3) + (c & 7) : c);
+  }
+};
+
 template <int KC>
 __device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16],
                                                 const h2 (&bot)[16]) {
-  constexpr int WPS = 16 * (32 * KC + 8);
+  constexpr int WPS = StripLds<KC>::WPS;
   const h2 qp = {0.25f16, 0.25f16};
   const h2 qn = {-0.25f16, -0.25f16};
   h2 t[4][4][2];
@@ -537,16 +554,35 @@ struct IntC {
 };
 
 // Two waves per SIMD: at most 256 registers per lane (U' takes 64 * KC).
+// Output staging: after act and the fp16 rounding, each item's 2 x 32 x C
+// output tile goes to LDS as [row][pixel][C] (16-byte channel groups of pixel x
+// at group index g ^ ((x >> 1) & (C/8 - 1)), which spreads the 8-byte writes of
+// the MFMA lanes over the banks). After the next barrier every thread moves
+// 16-byte groups to HBM, a wave covering whole 128-byte lines, and adds the
+// residual inputs on the way with loads of the same shape.
+template <int KC>
+struct StripStage {
+  static constexpr int C = 32 * KC;
+  static constexpr int G = C / 8;          // 16-byte groups per pixel
+  static constexpr int SBUF = 2 * 32 * C;  // halfs per staging buffer
+  __host__ __device__ static constexpr int at(int row, int x, int g) {
+    return (row * 32 + x) * C + ((g ^ ((x >> 1) & (G - 1))) << 3);
+  }
+};
+
 template <int KC, int ACT, int NSKIP>
 __global__ void __launch_bounds__(128 * KC) __attribute__((amdgpu_waves_per_eu(2, 2)))
 winograd_strip(StripArgs a) {
   constexpr int C = 32 * KC;   // input channels = output channels
-  constexpr int TS = C + 8;    // LDS halfs per tile row (16-byte pad)
-  constexpr int WPS = 16 * TS; // halfs per position
-  constexpr int VBUF = 16 * WPS;
+  constexpr int NT = 128 * KC; // threads
+  constexpr int WPS = StripLds<KC>::WPS;
+  constexpr int VBUF = StripLds<KC>::VBUF;
+  constexpr int SBUF = StripStage<KC>::SBUF;
+  constexpr int GR = StripStage<KC>::G;
   constexpr int QUADS = C / 4;
   constexpr int PX = 2 * C;    // bytes per pixel
-  extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
+  extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];  // 2 V' + 2 staging buffers
+  _Float16* const stg = vlds + 2 * VBUF;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -571,25 +607,37 @@ winograd_strip(StripArgs a) {
   // Input task: tile tt of the item, channels [4*tq, 4*tq + 4).
   const int tt = tid / QUADS;
   const int tq = tid - tt * QUADS;
-  // MFMA / epilogue lane: tile tcol; B rows 8*kq.. of each 32-channel chunk;
-  // output channels [ch0, ch0 + 4).
+  // MFMA lane: tile tcol; B rows 8*kq.. of each 32-channel chunk; output
+  // channels [ch0, ch0 + 4) of the tile's four pixels.
   const int tcol = lane & 15;
   const int kq = lane >> 4;
   const int ch0 = 16 * wave + 4 * kq;
   const f4 bias4 = *reinterpret_cast<const f4*>(a.bias + ch0);
-  _Float16* const vw0 = vlds + tt * TS + 4 * tq;
+  _Float16* const vw0 = vlds + StripLds<KC>::at(tt, 4 * tq);
   _Float16* const vw1 = vw0 + VBUF;
-  const _Float16* const vr0 = vlds + tcol * TS + 8 * kq;
-  const _Float16* const vr1 = vr0 + VBUF;
-  const uint32_t out_lane = (uint32_t)(2 * tcol * C + ch0) * 2;
+  const _Float16* vr0[KC];
+  const _Float16* vr1[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) {
+    vr0[kc] = vlds + StripLds<KC>::at(tcol, 32 * kc + 8 * kq);
+    vr1[kc] = vr0[kc] + VBUF;
+  }
+  // Staging write offset of (row 0, pixel 2*tcol); the other three pixels of
+  // the tile are +C, +32C, +33C halfs (same swizzle: x >> 1 == tcol).
+  const int sw0 = StripStage<KC>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
+  // Store phase: thread handles group sg of pixel sx in both rows.
+  const int sx = tid / GR;
+  const int sg = tid - sx * GR;
+  const int sr0 = StripStage<KC>::at(0, sx, sg);
+  const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;  // bytes from the row's first pixel
   const int64_t row_bytes = (int64_t)a.Wp * PX;
 
   int n, s, th;
   auto decode = [&](int item) {
-    const uint32_t sg = fdiv((uint32_t)item, a.fd_tiles_h);
-    th = item - (int)(sg * (uint32_t)a.tiles_h);
-    const uint32_t nn = fdiv(sg, a.fd_strips);
-    s = (int)(sg - nn * (uint32_t)a.n_strips);
+    const uint32_t sgl = fdiv((uint32_t)item, a.fd_tiles_h);
+    th = item - (int)(sgl * (uint32_t)a.tiles_h);
+    const uint32_t nn = fdiv(sgl, a.fd_strips);
+    s = (int)(sgl - nn * (uint32_t)a.n_strips);
     n = (int)nn;
   };
   // Byte offset of this thread's patch within a strip row; tiles past the
@@ -609,38 +657,60 @@ winograd_strip(StripArgs a) {
       }
   };
 
-  // One item: transform, barrier, loads for the next item of the strip, MFMA
-  // and epilogue. The next item's two new rows go into `top` (the rows the
-  // transform just consumed); past the last item of the run the row index is
-  // clamped to the last two rows of the padded image, which are loaded and
-  // never used, so the loop body has no data-dependent branch around a load.
-  h2 A[16], B[16];
-  auto body = [&](auto buf_tag, h2 (&top)[16], h2 (&bot)[16]) {
-    constexpr int BUF = decltype(buf_tag)::value;
-    _Float16* const vw = BUF ? vw1 : vw0;
-    const _Float16* const vr = BUF ? vr1 : vr0;
-    strip_transform<KC>(vw, top, bot);
-    lds_sync();
-
-    const bool vt = 16 * s + tcol < a.tiles_w;
-    const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + 32 * s + 1;
-    // Residual inputs of this item (in-bounds for every valid tile: the pixel
-    // right of / below the tile is at worst the zero border).
-    h4 sk[2][4];
+  // Coordinates of the item whose output sits in staging, and its residual
+  // inputs (loaded after the next item's barrier, consumed after that item's
+  // MFMA work).
+  int pn = 0, ps = 0, pth = 0;
+  h8 skr[2][2];
+  auto out_valid = [&](int row) {
+    return (32 * ps + sx < a.W) && (row == 0 || 2 * pth + 1 < a.H);
+  };
+  auto load_skips = [&]() {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sk[k][q] = h4{0, 0, 0, 0};
-    if (NSKIP > 0 && vt) {
+      for (int r = 0; r < 2; ++r) skr[k][r] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (NSKIP > 0) {
+      const int64_t pix0 = ((int64_t)pn * a.Hp + 2 * pth + 1) * a.Wp + 32 * ps + 1;
 #pragma unroll
       for (int k = 0; k < NSKIP; ++k) {
         const char* sb = reinterpret_cast<const char*>(k == 0 ? a.skip0 : a.skip1) + pix0 * PX;
-        sk[k][0] = *reinterpret_cast<const h4*>(sb + out_lane);
-        sk[k][1] = *reinterpret_cast<const h4*>(sb + out_lane + PX);
-        sk[k][2] = *reinterpret_cast<const h4*>(sb + row_bytes + out_lane);
-        sk[k][3] = *reinterpret_cast<const h4*>(sb + row_bytes + out_lane + PX);
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+          if (out_valid(r))
+            skr[k][r] = *reinterpret_cast<const h8*>(sb + r * row_bytes + s_lane);
       }
     }
+  };
+  auto store_phase = [&](auto buf_tag) {
+    constexpr int SB = decltype(buf_tag)::value;
+    const int64_t pix0 = ((int64_t)pn * a.Hp + 2 * pth + 1) * a.Wp + 32 * ps + 1;
+    char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      if (!out_valid(r)) continue;
+      h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C);
+      v += skr[0][r];
+      v += skr[1][r];
+      *reinterpret_cast<h8*>(ob + r * row_bytes + s_lane) = v;
+    }
+  };
+
+  // One item: transform, barrier, loads (the previous item's residual inputs,
+  // the next item's rows), MFMA work, store of the previous item's output,
+  // staging of this item's output.
+  // The next item's two new rows go into `top` (the rows the transform just
+  // consumed); past the last item of the run the row index is clamped to the
+  // last two rows of the padded image, which are loaded and never used, so the
+  // loop body has no data-dependent branch around a load.
+  h2 A[16], B[16];
+  auto body = [&](auto buf_tag, h2 (&top)[16], h2 (&bot)[16], bool store_prev) {
+    constexpr int BUF = decltype(buf_tag)::value;
+    _Float16* const vw = BUF ? vw1 : vw0;
+    const _Float16* const* vr = BUF ? vr1 : vr0;
+    strip_transform<KC>(vw, top, bot);
+    lds_sync();
+    if (store_prev) load_skips();
     {
       const int r = 2 * th + 4;
       load2(top, in_row(r < a.Hp - 2 ? r : a.Hp - 2));
@@ -651,48 +721,57 @@ winograd_strip(StripArgs a) {
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            u[p][kc], *reinterpret_cast<const h8*>(vr + p * WPS + kc * 32), acc, 0, 0, 0);
+            u[p][kc], *reinterpret_cast<const h8*>(vr[kc] + p * WPS), acc, 0, 0, 0);
       return acc;
     };
     const f4 z = {0, 0, 0, 0};
     const f4 m2 = {-2.0f, -2.0f, -2.0f, -2.0f};
-    f4 P[4], Q[4];
+    // Row by row, accumulated into the four outputs as each row completes.
+    f4 y00, y01, y10, y11;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      f4 P, Q;
       if (r == 1) {
         const f4 Y = mm(5, bias4);
         const f4 b = mm(6, Y);
-        P[1] = mm(4, b);
+        P = mm(4, b);
         const f4 c = mm(7, Y);
-        Q[1] = (c - b) + Y;
+        Q = (c - b) + Y;
       } else {
         const f4 X = mm(4 * r + 2, z);
         const f4 b = mm(4 * r + 1, X);
-        P[r] = mm(4 * r, b);
+        P = mm(4 * r, b);
         const f4 c = mm(4 * r + 3, b);
-        Q[r] = __builtin_elementwise_fma(X, m2, c);
+        Q = __builtin_elementwise_fma(X, m2, c);
+      }
+      if (r == 0) {
+        y00 = P;
+        y01 = Q;
+      } else if (r == 1) {
+        y00 += P;
+        y01 += Q;
+        y10 = P;
+        y11 = Q;
+      } else if (r == 2) {
+        y00 += P;
+        y01 += Q;
+        y10 -= P;
+        y11 -= Q;
+      } else {
+        y10 -= P;
+        y11 -= Q;
       }
     }
-    const f4 y00 = (P[0] + P[1]) + P[2];
-    const f4 y01 = (Q[0] + Q[1]) + Q[2];
-    const f4 y10 = (P[1] - P[2]) - P[3];
-    const f4 y11 = (Q[1] - Q[2]) - Q[3];
-
-    if (vt) {
-      const bool w1 = 2 * (16 * s + tcol) + 1 < a.W;
-      const bool h1 = 2 * th + 1 < a.H;
-      char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
-      *reinterpret_cast<h4*>(ob + out_lane) = strip_epi4<ACT>(y00, sk[0][0], sk[1][0]);
-      if (w1)
-        *reinterpret_cast<h4*>(ob + out_lane + PX) = strip_epi4<ACT>(y01, sk[0][1], sk[1][1]);
-      if (h1) {
-        *reinterpret_cast<h4*>(ob + row_bytes + out_lane) =
-            strip_epi4<ACT>(y10, sk[0][2], sk[1][2]);
-        if (w1)
-          *reinterpret_cast<h4*>(ob + row_bytes + out_lane + PX) =
-              strip_epi4<ACT>(y11, sk[0][3], sk[1][3]);
-      }
-    }
+    if (store_prev) store_phase(IntC<BUF ^ 1>{});
+    const h4 zh = {0, 0, 0, 0};
+    _Float16* sw = stg + BUF * SBUF + sw0;
+    *reinterpret_cast<h4*>(sw) = strip_epi4<ACT>(y00, zh, zh);
+    *reinterpret_cast<h4*>(sw + C) = strip_epi4<ACT>(y01, zh, zh);
+    *reinterpret_cast<h4*>(sw + 32 * C) = strip_epi4<ACT>(y10, zh, zh);
+    *reinterpret_cast<h4*>(sw + 33 * C) = strip_epi4<ACT>(y11, zh, zh);
+    pn = n;
+    ps = s;
+    pth = th;
     ++th;
   };
 
@@ -706,14 +785,24 @@ winograd_strip(StripArgs a) {
     }
     load2(A, in_row(2 * th));
     load2(B, in_row(2 * th + 2));
-    // The buffer parity restarts with each run; this barrier keeps the first
-    // transform of the run behind every wave's last MFMA reads.
+    // Buffer parity restarts with each run; this barrier keeps the first
+    // transform and staging writes of the run behind every wave's last reads.
     lds_sync();
-    for (int k = len;;) {
-      body(IntC<0>{}, A, B);
-      if (--k == 0) break;
-      body(IntC<1>{}, B, A);
-      if (--k == 0) break;
+    for (int k = len, first = 1;; first = 0) {
+      body(IntC<0>{}, A, B, !first);
+      if (--k == 0) {
+        load_skips();
+        lds_sync();
+        store_phase(IntC<0>{});
+        break;
+      }
+      body(IntC<1>{}, B, A, true);
+      if (--k == 0) {
+        load_skips();
+        lds_sync();
+        store_phase(IntC<1>{});
+        break;
+      }
     }
     it += len;
   }
@@ -1063,7 +1152,9 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
                            : strip_kernel_act<2>(w.epi.act, nskip);
   if (fn == nullptr) return hipErrorInvalidValue;
   const int threads = 128 * kc;
-  const size_t lds = (size_t)2 * 16 * 16 * (32 * kc + 8) * 2;
+  const size_t lds = (size_t)2 *
+                     (kc == 1 ? StripLds<1>::VBUF + StripStage<1>::SBUF
+                              : StripLds<2>::VBUF + StripStage<2>::SBUF) * 2;
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
