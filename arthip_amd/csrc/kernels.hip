@@ -44,6 +44,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 // Workgroup barrier that first retires this wave's outstanding LDS traffic.
 // s_barrier alone orders control flow only; a ds_write still in flight could
@@ -659,11 +660,25 @@ winograd_strip(StripArgs a) {
 
   // Coordinates of the item whose output sits in staging, and its residual
   // inputs (loaded after the next item's barrier, consumed after that item's
-  // MFMA work).
+  // MFMA work). Residual loads and output stores go through buffer resources
+  // spanning the item's two output rows: pixels past the right edge and the
+  // second row past the bottom get an offset beyond the resource's size, which
+  // the hardware drops (stores) or reads as zero (loads). Every thread thus
+  // issues the same number of memory instructions on every path, and the
+  // waits before the next transform count exactly the input-row loads instead
+  // of also waiting on this item's stores.
   int pn = 0, ps = 0, pth = 0;
+  bool have_prev = false;  // uniform: staging holds an item not yet stored
   h8 skr[2][2];
-  auto out_valid = [&](int row) {
-    return (32 * ps + sx < a.W) && (row == 0 || 2 * pth + 1 < a.H);
+  constexpr uint32_t kOob = 0x80000000u;
+  const uint32_t rb32 = (uint32_t)row_bytes;
+  const int n_rec = (int)(rb32 + 32 * PX);
+  auto st_off = [&](int r) -> uint32_t {
+    const bool ok = have_prev && (32 * ps + sx < a.W) && (r == 0 || 2 * pth + 1 < a.H);
+    return ok ? (uint32_t)r * rb32 + s_lane : kOob;
+  };
+  auto item_pix = [&]() {
+    return ((int64_t)pn * a.Hp + 2 * pth + 1) * a.Wp + 32 * ps + 1;
   };
   auto load_skips = [&]() {
 #pragma unroll
@@ -671,46 +686,48 @@ winograd_strip(StripArgs a) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) skr[k][r] = h8{0, 0, 0, 0, 0, 0, 0, 0};
     if (NSKIP > 0) {
-      const int64_t pix0 = ((int64_t)pn * a.Hp + 2 * pth + 1) * a.Wp + 32 * ps + 1;
+      const int64_t pix0 = item_pix();
+      const uint32_t o0 = st_off(0), o1 = st_off(1);
 #pragma unroll
       for (int k = 0; k < NSKIP; ++k) {
         const char* sb = reinterpret_cast<const char*>(k == 0 ? a.skip0 : a.skip1) + pix0 * PX;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-          if (out_valid(r))
-            skr[k][r] = *reinterpret_cast<const h8*>(sb + r * row_bytes + s_lane);
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)sb, (short)0, n_rec, 0x00020000);
+        skr[k][0] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, o0, 0, 0));
+        skr[k][1] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rs, o1, 0, 0));
       }
     }
   };
-  auto store_phase = [&](auto buf_tag) {
-    constexpr int SB = decltype(buf_tag)::value;
-    const int64_t pix0 = ((int64_t)pn * a.Hp + 2 * pth + 1) * a.Wp + 32 * ps + 1;
-    char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
+  auto store_phase = [&](int SB) {
+    char* ob = reinterpret_cast<char*>(a.out) + item_pix() * PX;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, n_rec, 0x00020000);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      if (!out_valid(r)) continue;
       h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C);
       v += skr[0][r];
       v += skr[1][r];
-      *reinterpret_cast<h8*>(ob + r * row_bytes + s_lane) = v;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs, st_off(r), 0, 0);
     }
   };
 
   // One item: transform, barrier, loads (the previous item's residual inputs,
   // the next item's rows), MFMA work, store of the previous item's output,
-  // staging of this item's output.
+  // staging of this item's output. The first item of a run has no previous
+  // item in staging (the run start drained it); its store phase is issued with
+  // out-of-range offsets, keeping the instruction count of every path equal.
   // The next item's two new rows go into `top` (the rows the transform just
   // consumed); past the last item of the run the row index is clamped to the
   // last two rows of the padded image, which are loaded and never used, so the
   // loop body has no data-dependent branch around a load.
   h2 A[16], B[16];
-  auto body = [&](auto buf_tag, h2 (&top)[16], h2 (&bot)[16], bool store_prev) {
+  auto body = [&](auto buf_tag, h2 (&top)[16], h2 (&bot)[16]) {
     constexpr int BUF = decltype(buf_tag)::value;
     _Float16* const vw = BUF ? vw1 : vw0;
     const _Float16* const* vr = BUF ? vr1 : vr0;
     strip_transform<KC>(vw, top, bot);
     lds_sync();
-    if (store_prev) load_skips();
+    load_skips();
     {
       const int r = 2 * th + 4;
       load2(top, in_row(r < a.Hp - 2 ? r : a.Hp - 2));
@@ -762,7 +779,7 @@ winograd_strip(StripArgs a) {
         y11 -= Q;
       }
     }
-    if (store_prev) store_phase(IntC<BUF ^ 1>{});
+    store_phase(BUF ^ 1);
     const h4 zh = {0, 0, 0, 0};
     _Float16* sw = stg + BUF * SBUF + sw0;
     *reinterpret_cast<h4*>(sw) = strip_epi4<ACT>(y00, zh, zh);
@@ -772,10 +789,15 @@ winograd_strip(StripArgs a) {
     pn = n;
     ps = s;
     pth = th;
+    have_prev = true;
     ++th;
   };
 
-  // Runs: maximal stretches of the item range within one strip.
+  // Runs: maximal stretches of the item range within one strip. Each run
+  // starts by storing the previous run's last item (after its initial loads,
+  // so that the loop is entered with the same memory-instruction order as its
+  // back edge: input rows, then two stores); the range ends with a final drain.
+  int last_buf = 0;
   for (int it = begin; it < end;) {
     decode(it);
     const int len = min(end - it, a.tiles_h - th);
@@ -785,27 +807,25 @@ winograd_strip(StripArgs a) {
     }
     load2(A, in_row(2 * th));
     load2(B, in_row(2 * th + 2));
-    // Buffer parity restarts with each run; this barrier keeps the first
-    // transform and staging writes of the run behind every wave's last reads.
+    load_skips();
+    // Orders the previous run's staging writes before the store below and its
+    // last V' reads before this run's first transform (buffer parity restarts).
     lds_sync();
-    for (int k = len, first = 1;; first = 0) {
-      body(IntC<0>{}, A, B, !first);
-      if (--k == 0) {
-        load_skips();
-        lds_sync();
-        store_phase(IntC<0>{});
-        break;
-      }
-      body(IntC<1>{}, B, A, true);
-      if (--k == 0) {
-        load_skips();
-        lds_sync();
-        store_phase(IntC<1>{});
-        break;
-      }
+    store_phase(last_buf);
+    have_prev = false;
+    for (int k = len;;) {
+      body(IntC<0>{}, A, B);
+      last_buf = 0;
+      if (--k == 0) break;
+      body(IntC<1>{}, B, A);
+      last_buf = 1;
+      if (--k == 0) break;
     }
     it += len;
   }
+  load_skips();
+  lds_sync();
+  store_phase(last_buf);
 }
 
 // ---------------------------------------------------------------------------
