@@ -84,6 +84,23 @@ struct StripArgs {
   FastDiv fd_tiles_h, fd_strips;
 };
 
+// Direct 3x3 conv on MFMA for M <= 16 outputs written to the boundary NCHW
+// layout (conv3x3_narrow in kernels.hip). Work items are 1 output row x 64
+// pixels, ordered (n, 64-pixel segment, row) with the row fastest.
+struct NarrowArgs {
+  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C]
+  const uint16_t* w;   // narrow taps (narrow_packed_halfs layout)
+  const float* bias;   // [>= 16] fp32, zero padded
+  void* out;           // NCHW [N][Cout][H*b][W*b], fp16 or fp32
+  int32_t N, H, W, Hp, Wp, M;
+  int32_t act, do_clip;
+  float clip_lo, clip_hi;
+  int32_t dts_b, cout;       // DepthToSpace block (1 = none); Cout = M / b^2
+  int32_t n_seg, n_items;    // ceil(W / 64); N * n_seg * H
+  FastDiv fd_H, fd_seg;
+  int64_t img_bytes;         // bytes of one output image (< 2^31)
+};
+
 // Direct 3x3 conv for a single input channel (the model's head conv).
 struct DirectArgs {
   const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][1]

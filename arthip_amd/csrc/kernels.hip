@@ -828,6 +828,257 @@ winograd_strip(StripArgs a) {
   store_phase(last_buf);
 }
 
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// One 16-byte-per-lane global -> LDS copy: lane l of the wave writes LDS bytes
+// [m0 + 16 l, m0 + 16 l + 16) from gbase + voff. Inline assembly, so the
+// compiler neither tracks it nor inserts waits for it; the kernels count it.
+__device__ __forceinline__ void dma16(uint32_t m0, const char* gbase, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(m0), "v"(voff), "s"(gbase)
+      : "memory");
+}
+
+// Waits until at most N of this wave's vector-memory instructions are
+// outstanding (they complete in issue order). Inline assembly with a memory
+// clobber, so that the compiler moves no memory access across it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Direct 3x3 conv on MFMA for narrow outputs (M <= 16), boundary layout
+// ---------------------------------------------------------------------------
+//
+// The tail of the upscaler (64 -> 4 channels, then DepthToSpace) has too few
+// outputs for the Winograd transform to pay: its cost is per input channel.
+// Here each wave computes 16 output pixels x 16 channel slots with
+// v_mfma_f32_16x16x32_f16, A = input pixels (one 3x3 tap, 32 channels: 16 B
+// per lane straight from LDS), B = the taps (registers, 9 * KC fragments).
+// A workgroup walks down a 64-pixel-wide segment; input rows (66 pixels with
+// the halo) stream into an LDS ring by global_load_lds, D rows ahead. Each
+// item's outputs go through a double-buffered fp32 tile in LDS and leave as
+// DepthToSpace-ordered NCHW rows after the next barrier.
+//
+// Per item k (output row h0 + k; ring row j = padded input row h0 + j):
+//   store item k-1 (from tile (k-1)&1)          4 element stores per thread
+//   DMA ring row k + D + 2 -> slot (k+D+2) % R   NI instructions per wave
+//   MFMA over ring rows k .. k+2, epilogue -> tile k&1
+//   wait for ring row k + 3, barrier
+// Ring row k + 3 was issued at item k + 1 - D, so (D - 1) * (NI + 4) of this
+// wave's vector-memory instructions follow it; the prologue issues its rows in
+// the same (4 stores, NI DMA) pattern so that the count holds from item 0.
+template <int KC>
+struct NarrowRing {
+  static constexpr int C = 32 * KC;
+  static constexpr int PXB = 2 * C;                // bytes per pixel
+  static constexpr int ROWB = 66 * PXB;            // 64 pixels + 2 halo
+  static constexpr int D = KC == 1 ? 6 : (KC == 2 ? 5 : 2);
+  static constexpr int NSLOT = D + 3;
+  static constexpr int CHUNKS = ROWB / 16;
+  static constexpr int NI = (CHUNKS + 255) / 256;  // DMA instructions per wave per row
+  static constexpr int G = 4 * KC;                 // 16-byte channel groups per pixel
+  static constexpr int TILE = 16 * 64;             // fp32 output tile (16 channels x 64 px)
+  static constexpr int WAIT = (D - 1) * (NI + 4);
+  // Group g of pixel x sits at g ^ swz(x): the 16 lanes of an A read (16
+  // consecutive pixels, one group) then cover all 64 banks.
+  __host__ __device__ static constexpr int swz(int x) { return KC == 2 ? (x >> 1) & 7 : (x >> 2) & 3; }
+  __host__ __device__ static constexpr int first_chunk(int q) { return q * CHUNKS / (4 * NI); }
+  static constexpr size_t lds_bytes() { return (size_t)NSLOT * ROWB + 2 * TILE * 4; }
+};
+
+template <int KC, bool F32>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+conv3x3_narrow(NarrowArgs a) {
+  using R = NarrowRing<KC>;
+  extern __shared__ __attribute__((aligned(16))) float nlds[];  // tiles | ring
+  float* const tile = nlds;
+  char* const ring = reinterpret_cast<char*>(nlds + 2 * R::TILE);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+
+  const int G = gridDim.x;
+  const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int begin = (int)((int64_t)a.n_items * slot / G);
+  const int end = (int)((int64_t)a.n_items * (slot + 1) / G);
+  if (begin >= end) return;  // uniform across the workgroup
+
+  h8 wb[9][KC];
+  {
+    const h8* wp = reinterpret_cast<const h8*>(a.w) + lane;
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) wb[t][kc] = wp[(t * KC + kc) * 64];
+  }
+  const int nch = lane & 15;  // output channel slot of this lane's D column
+  const float bias = a.bias[nch];
+  const int m = lane & 15, kq = lane >> 4;
+  // A reads: pixel 16*wave + m + dx of a ring row, channel group 4*kc + kq.
+  uint32_t aoff[3][KC];
+#pragma unroll
+  for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int x = 16 * wave + m + dx;
+      aoff[dx][kc] = (uint32_t)(x * R::PXB + (((4 * kc + kq) ^ R::swz(x)) << 4));
+    }
+  // Tile write: channel nch, pixels 16*wave + 4*kq .. +3.
+  const int twr = nch * 64 + 16 * wave + 4 * kq;
+
+  // Store phase: this thread's four output elements of an item (element
+  // E = ((c*b + r)*64b + xq)) -> tile index and image offset (bytes, without
+  // the item's row/segment part), or nothing past the M*64 elements.
+  const int b = a.dts_b;
+  const int64_t Wo = (int64_t)a.W * b;
+  const int64_t Ho = (int64_t)a.H * b;
+  constexpr int ELEM = F32 ? 4 : 2;
+  int s_tile[4], s_x[4];
+  uint32_t s_off[4];
+  bool s_live[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * tid + i;
+    s_live[i] = e < a.M * 64;
+    const int seg = 64 * b;
+    const int cr = e / seg;
+    const int xq = e - cr * seg;
+    const int c = cr / b, r = cr - (cr / b) * b;
+    const int x = xq / b, q = xq - (xq / b) * b;
+    const int k = (r * b + q) * a.cout + c;
+    s_tile[i] = s_live[i] ? k * 64 + x : 0;
+    s_x[i] = x;
+    s_off[i] = s_live[i] ? (uint32_t)(((int64_t)c * Ho + r) * Wo + xq) * ELEM : 0u;
+  }
+  constexpr uint32_t kOob = 0x80000000u;
+
+  int n = 0, sg = 0, h0 = 0;
+  auto decode = [&](int item) {
+    const uint32_t t = fdiv((uint32_t)item, a.fd_H);
+    h0 = item - (int)(t * (uint32_t)a.H);
+    const uint32_t nn = fdiv(t, a.fd_seg);
+    sg = (int)(t - nn * (uint32_t)a.n_seg);
+    n = (int)nn;
+  };
+  // DMA lane offsets for this segment (relative to a ring row's first pixel).
+  uint32_t doff[R::NI];
+  int dcnt[R::NI];
+  auto setup_dma = [&]() {
+    const int xmax = a.Wp - 1 - 64 * sg;
+#pragma unroll
+    for (int j = 0; j < R::NI; ++j) {
+      const int q = R::NI * wave + j;
+      const int c0 = R::first_chunk(q);
+      dcnt[j] = R::first_chunk(q + 1) - c0;
+      int c = c0 + lane;
+      if (c >= R::CHUNKS) c = R::CHUNKS - 1;
+      const int x = c / R::G;
+      const int gp = c - x * R::G;
+      const int g = gp ^ R::swz(x);
+      doff[j] = (uint32_t)((x > xmax ? xmax : x) * R::PXB + g * 16);
+    }
+  };
+  // Ring row j of the run (padded input row h0 + j, clamped) -> slot j % NSLOT.
+  auto dma_row = [&](int j) {
+    int pr = h0 + j;
+    if (pr > a.Hp - 1) pr = a.Hp - 1;
+    const char* gb = reinterpret_cast<const char*>(a.in) +
+                     (((int64_t)n * a.Hp + pr) * a.Wp + 64 * sg) * R::PXB;
+    const uint32_t sb = lds_byte_addr(ring) + (uint32_t)((j % R::NSLOT) * R::ROWB);
+#pragma unroll
+    for (int q = 0; q < R::NI; ++q) {
+      const uint32_t m0 = sb + (uint32_t)R::first_chunk(R::NI * wave + q) * 16;
+      if (lane < dcnt[q]) dma16(m0, gb, doff[q]);
+    }
+  };
+  // Four element stores of the item (pn, ps, ph) from tile buffer tb; every
+  // thread issues exactly four (out-of-range offsets when absent).
+  int pn = 0, ps = 0, ph = 0;
+  auto store_item = [&](int tb, bool live) {
+    char* ob = reinterpret_cast<char*>(a.out) + (int64_t)pn * a.img_bytes;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, (int)a.img_bytes, 0x00020000);
+    const uint32_t item_off = (uint32_t)(((int64_t)ph * b * Wo + (int64_t)64 * ps * b) * ELEM);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = tile[tb * R::TILE + s_tile[i]];
+      const bool ok = live && s_live[i] && (64 * ps + s_x[i] < a.W);
+      const uint32_t off = ok ? item_off + s_off[i] : kOob;
+      if (F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, off, 0, 0);
+      } else {
+        const _Float16 hv = (_Float16)v;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, hv), rs, off, 0, 0);
+      }
+    }
+  };
+
+  int last_tb = 0;
+  bool have_prev = false;
+  for (int it = begin; it < end;) {
+    decode(it);
+    const int len = min(end - it, a.H - h0);
+    // Retire the previous run (stray ring rows included), store its last item.
+    wait_vmcnt<0>();
+    lds_sync();
+    store_item(last_tb, have_prev);
+    have_prev = false;
+    setup_dma();
+#pragma unroll 1
+    for (int j = 0; j < R::D + 2; ++j) {
+      store_item(0, false);  // keeps the per-row instruction pattern of the loop
+      dma_row(j);
+    }
+    wait_vmcnt<R::WAIT>();  // ring rows 0..2
+    lds_sync();
+#pragma unroll 1
+    for (int k = 0; k < len; ++k) {
+      store_item((k + 1) & 1, have_prev);
+      dma_row(k + R::D + 2);
+      f4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy) {
+        const char* rowp = ring + ((k + dy) % R::NSLOT) * R::ROWB;
+#pragma unroll
+        for (int dx = 0; dx < 3; ++dx)
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                *reinterpret_cast<const h8*>(rowp + aoff[dx][kc]), wb[dy * 3 + dx][kc], acc, 0,
+                0, 0);
+      }
+      f4 y;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float t = apply_act(acc[v] + bias, a.act);
+        if (a.do_clip) t = apply_clip(t, a.clip_lo, a.clip_hi);
+        y[v] = t;
+      }
+      *reinterpret_cast<f4*>(tile + (k & 1) * R::TILE + twr) = y;
+      pn = n;
+      ps = sg;
+      ph = h0 + k;
+      have_prev = true;
+      last_tb = k & 1;
+      wait_vmcnt<R::WAIT>();  // ring row k + 3
+      lds_sync();
+    }
+    it += len;
+  }
+  wait_vmcnt<0>();
+  lds_sync();
+  store_item(last_tb, have_prev);
+}
+
 // ---------------------------------------------------------------------------
 // Direct 3x3 conv with one input channel (head conv)
 // ---------------------------------------------------------------------------
@@ -1193,7 +1444,80 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
 
 }  // namespace
 
+namespace {
+
+using NarrowKernel = void (*)(NarrowArgs);
+
+// conv3x3_narrow covers boundary-layout outputs with M <= 16 and no residual
+// inputs (the model's tail conv, with or without DepthToSpace and Clip).
+bool narrow_launch_eligible(const WinoArgs& w) {
+  if (!narrow_eligible(w.C, w.M)) return false;
+  if (w.epi.out_kind != kOutNchwF16 && w.epi.out_kind != kOutNchwF32) return false;
+  if (w.epi.skip0 != nullptr || w.epi.skip1 != nullptr) return false;
+  const int b = w.epi.dts_b >= 2 ? w.epi.dts_b : 1;
+  if (w.M % (b * b) != 0) return false;
+  const int64_t elem = w.epi.out_kind == kOutNchwF32 ? 4 : 2;
+  const int64_t img = (int64_t)w.M * w.H * w.W * elem;  // Cout * (H b) * (W b)
+  return img < ((int64_t)1 << 31);
+}
+
+template <int KC>
+hipError_t launch_narrow_kc(const NarrowArgs& a, bool f32, hipStream_t s) {
+  NarrowKernel fn = f32 ? conv3x3_narrow<KC, true> : conv3x3_narrow<KC, false>;
+  const size_t lds = NarrowRing<KC>::lds_bytes();
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, lds) != hipSuccess || occ < 1)
+    occ = 1;
+  int64_t grid = (int64_t)cu_count() * occ;
+  if (grid > a.n_items) grid = a.n_items;
+  grid = (grid + 7) / 8 * 8;
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), lds, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_narrow(const WinoArgs& w, hipStream_t s) {
+  NarrowArgs a{};
+  a.in = w.in;
+  a.w = w.u + winograd_u_halfs(w.C, w.M);
+  a.bias = w.epi.bias;
+  a.out = w.epi.out;
+  a.N = w.N;
+  a.H = w.H;
+  a.W = w.W;
+  a.Hp = (int32_t)padded_rows(w.H);
+  a.Wp = (int32_t)padded_cols(w.W);
+  a.M = w.M;
+  a.act = w.epi.act;
+  a.do_clip = w.epi.do_clip;
+  a.clip_lo = w.epi.clip_lo;
+  a.clip_hi = w.epi.clip_hi;
+  a.dts_b = w.epi.dts_b >= 2 ? w.epi.dts_b : 1;
+  a.cout = w.M / (a.dts_b * a.dts_b);
+  a.n_seg = (w.W + 63) / 64;
+  const int64_t items = (int64_t)w.N * a.n_seg * w.H;
+  if (items >= (int64_t)1 << 31) return hipErrorInvalidValue;
+  a.n_items = (int32_t)items;
+  a.fd_H = make_fastdiv((uint32_t)w.H);
+  a.fd_seg = make_fastdiv((uint32_t)a.n_seg);
+  const bool f32 = w.epi.out_kind == kOutNchwF32;
+  a.img_bytes = (int64_t)w.M * w.H * w.W * (f32 ? 4 : 2);
+  switch (w.C / 32) {
+    case 1: return launch_narrow_kc<1>(a, f32, s);
+    case 2: return launch_narrow_kc<2>(a, f32, s);
+    case 3: return launch_narrow_kc<3>(a, f32, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
 hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
+  if (narrow_launch_eligible(a)) return launch_narrow(a, s);
   if (strip_eligible(a)) return launch_strip(a, s);
   const WinoGeom g = winograd_geom(a.C, a.M);
   a.n_ob = g.n_ob;

@@ -6,15 +6,36 @@
 
 namespace arthip {
 
-size_t winograd_packed_halfs(int C, int M) {
+bool narrow_eligible(int C, int M) { return C % 32 == 0 && C <= 96 && M >= 1 && M <= 16; }
+
+size_t narrow_packed_halfs(int C, int M) {
+  return narrow_eligible(C, M) ? static_cast<size_t>(9) * (C / 32) * 64 * 8 : 0;
+}
+
+size_t winograd_u_halfs(int C, int M) {
   const WinoGeom g = winograd_geom(C, M);
   return static_cast<size_t>(g.n_ob) * 16 * g.kc * 64 * 8;
+}
+
+size_t winograd_packed_halfs(int C, int M) {
+  return winograd_u_halfs(C, M) + narrow_packed_halfs(C, M);
 }
 
 void winograd_pack(const float* w, int M, int C, uint16_t* out) {
   const WinoGeom g = winograd_geom(C, M);
   const size_t total = winograd_packed_halfs(C, M);
   std::memset(out, 0, total * sizeof(uint16_t));
+  if (narrow_eligible(C, M)) {
+    uint16_t* nb = out + winograd_u_halfs(C, M);
+    const int kcn = C / 32;
+    for (int n = 0; n < M; ++n)
+      for (int c = 0; c < C; ++c)
+        for (int t = 0; t < 9; ++t) {
+          const int kc = c / 32, q = (c % 32) / 8, e = c % 8;
+          const size_t idx = ((static_cast<size_t>(t) * kcn + kc) * 64 + n + 16 * q) * 8 + e;
+          nb[idx] = f32_to_f16(w[(static_cast<size_t>(n) * C + c) * 9 + t]);
+        }
+  }
   // G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]]; U = G g G^T in double,
   // scaled by 4 (exact), rounded once to fp16.
   static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};

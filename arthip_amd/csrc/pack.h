@@ -21,8 +21,18 @@ struct WinoGeom {
 WinoGeom winograd_geom(int C, int M);
 int direct_g8(int M);
 
-// Halfs in the packed U' buffer: [n_ob][16 positions][kc][64 lanes][8].
+// Convs with C % 32 == 0 (C <= 96) and M <= 16 can also run as a direct conv
+// on MFMA (conv3x3_narrow, used for boundary outputs such as the model's tail).
+bool narrow_eligible(int C, int M);
+// Halfs of the narrow-kernel taps: [9 taps][kc][64 lanes][8], lane = n + 16*q
+// holding w[n][32*kc + 8*q + e][tap] (v_mfma_f32_16x16x32_f16 B-operand order).
+size_t narrow_packed_halfs(int C, int M);
+
+// Halfs in the packed buffer: U' as [n_ob][16 positions][kc][64 lanes][8],
+// followed by the narrow taps when narrow_eligible(C, M).
 size_t winograd_packed_halfs(int C, int M);
+// Halfs of the U' part alone (offset of the narrow taps).
+size_t winograd_u_halfs(int C, int M);
 // w is OIHW [M][C][3][3] fp32 (exact fp16 values from the model).
 void winograd_pack(const float* w, int M, int C, uint16_t* out);
 

@@ -104,3 +104,35 @@ def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, str(HEADER.parents[1] / "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode != 0 and "one GPU" in r.stderr
+
+
+def test_narrow_pack_layout():
+    """C % 32 == 0 and M <= 16: the packed buffer continues after U' with the
+    direct-conv taps [tap][kc][lane][e] = w[n][32*kc + 8*(lane // 16) + e][tap],
+    n = lane % 16 (v_mfma_f32_16x16x32_f16 B-operand order), zero for n >= M."""
+    lib = _lib.lib()
+    rng = np.random.default_rng(7)
+    for c_in, m_out in [(64, 4), (32, 4), (96, 16), (64, 9)]:
+        w = (rng.standard_normal((m_out, c_in, 3, 3)) * 0.2).astype(np.float16)
+        n_u = lib.arthip_conv3x3_packed_halfs(m_out, c_in)
+        kc = c_in // 32
+        u_part = ((m_out + 15) // 16) * 16 * kc * 64 * 8
+        assert n_u == u_part + 9 * kc * 64 * 8
+        n_b = lib.arthip_conv3x3_bias_len(m_out)
+        u = np.zeros(n_u, np.uint16)
+        b = np.zeros(n_b, np.float32)
+        rc = lib.arthip_conv3x3_pack(
+            w.view(np.uint16).ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), None, m_out, c_in,
+            u.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n_u,
+            b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n_b)
+        assert rc == 0
+        nb = u[u_part:].view(np.float16).reshape(9, kc, 64, 8)
+        want = np.zeros((9, kc, 64, 8), np.float16)
+        for lane in range(64):
+            n, q = lane % 16, lane // 16
+            if n >= m_out:
+                continue
+            for k in range(kc):
+                for e in range(8):
+                    want[:, k, lane, e] = w[n, 32 * k + 8 * q + e].reshape(9)
+        np.testing.assert_array_equal(nb, want)
