@@ -1177,6 +1177,162 @@ __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
   }
 }
 
+// Row-segment variant for the fast epilogue (padded NHWC output, M % 8 == 0):
+// a work item is one output row x SEG pixels, SEG = 4 * 256 / G8. The three
+// input rows of the next item are loaded into registers while the current
+// item computes and then stored to the other of two LDS buffers (one barrier
+// per item). Thread t computes pixels 4q .. 4q+3 (q = t / G8) for channels
+// 8g .. 8g+7 (g = t % G8) from a 3 x 6 window read from LDS, and stores the four
+// 16-byte pixel vectors through a buffer resource spanning the segment's valid
+// pixels (stores past the right edge are dropped by its range check). The
+// stores take the nontemporal policy: measured at 1080p the head conv goes from
+// 81 to 75 us and the next conv, which reads this output, from 157 to 145 us.
+template <int G8>
+struct HeadSeg {
+  static constexpr int SEG = 4 * 256 / G8;
+  static constexpr int ROW = SEG + 4;           // LDS halfs per input row (SEG + 2 used)
+  static constexpr int NV = (3 * (SEG + 2) + 255) / 256;  // input values per thread
+};
+
+template <int G8>
+__global__ void __launch_bounds__(256) direct_conv_c1_rows(DirectArgs a, int n_seg, int n_items,
+                                                           FastDiv fd_seg, FastDiv fd_H) {
+  using S = HeadSeg<G8>;
+  __shared__ __attribute__((aligned(16))) _Float16 rows[2][3 * S::ROW];
+  const int tid = threadIdx.x;
+  const int g = tid % G8;
+  const int q = tid / G8;
+  const int ch0 = 8 * g;
+  const bool live = ch0 < a.M;
+  h2 wr[8][5];
+  {
+    const h2* wp = reinterpret_cast<const h2*>(a.w) + (size_t)g * 40;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int k = 0; k < 5; ++k) wr[c][k] = live ? wp[c * 5 + k] : h2{0, 0};
+  }
+  f4 b0 = {0, 0, 0, 0}, b1 = b0;
+  if (live) {
+    b0 = *reinterpret_cast<const f4*>(a.epi.bias + ch0);
+    b1 = *reinterpret_cast<const f4*>(a.epi.bias + ch0 + 4);
+  }
+  const _Float16* in = reinterpret_cast<const _Float16*>(a.in);
+
+  const int G = gridDim.x;
+  const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int begin = (int)((int64_t)n_items * slot / G);
+  const int end = (int)((int64_t)n_items * (slot + 1) / G);
+  if (begin >= end) return;  // uniform across the workgroup
+
+  auto coords = [&](int item, int& n, int& h, int& x0) {
+    const uint32_t t = fdiv((uint32_t)item, fd_seg);
+    x0 = (item - (int)(t * (uint32_t)n_seg)) * S::SEG;
+    const uint32_t nn = fdiv(t, fd_H);
+    h = (int)(t - nn * (uint32_t)a.H);
+    n = (int)nn;
+  };
+  // Input values of an item: element e = r * (SEG + 2) + x of padded rows
+  // h .. h+2, padded columns x0 .. x0 + SEG + 1 (clamped to the row).
+  _Float16 v[S::NV];
+  auto load_item = [&](int item) {
+    int n, h, x0;
+    coords(item, n, h, x0);
+#pragma unroll
+    for (int i = 0; i < S::NV; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / (S::SEG + 2);
+      int x = x0 + e - r * (S::SEG + 2);
+      if (x > a.Wp - 1) x = a.Wp - 1;
+      v[i] = e < 3 * (S::SEG + 2) ? in[((int64_t)n * a.Hp + h + r) * a.Wp + x] : (_Float16)0.0f;
+    }
+  };
+  auto store_item = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < S::NV; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e / (S::SEG + 2);
+      if (e < 3 * (S::SEG + 2)) rows[buf][r * S::ROW + e - r * (S::SEG + 2)] = v[i];
+    }
+  };
+
+  load_item(begin);
+  store_item(0);
+  if (begin + 1 < end) load_item(begin + 1);
+  __syncthreads();
+  for (int it = begin, buf = 0; it < end; ++it, buf ^= 1) {
+    int n, h, x0;
+    coords(it, n, h, x0);
+    // 3 x 6 window of pixels 4q .. 4q+3.
+    _Float16 x[3][6];
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      const _Float16* rp = &rows[buf][r * S::ROW + 4 * q];
+      const h4 lo = *reinterpret_cast<const h4*>(rp);
+      const h2 hi = *reinterpret_cast<const h2*>(rp + 4);
+      x[r][0] = lo[0]; x[r][1] = lo[1]; x[r][2] = lo[2]; x[r][3] = lo[3];
+      x[r][4] = hi[0]; x[r][5] = hi[1];
+    }
+    char* ob = reinterpret_cast<char*>(a.epi.out) +
+               (((int64_t)n * a.Hp + h + 1) * a.Wp + x0 + 1) * a.M * 2;
+    const int valid = min(S::SEG, a.W - x0);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, valid * a.M * 2, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h2 xv[5] = {h2{x[0][j], x[0][j + 1]}, h2{x[0][j + 2], x[1][j]},
+                        h2{x[1][j + 1], x[1][j + 2]}, h2{x[2][j], x[2][j + 1]},
+                        h2{x[2][j + 2], (_Float16)0.0f}};
+      f4 acc0, acc1;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+          s0 = __builtin_amdgcn_fdot2(xv[k], wr[c][k], s0, false);
+          s1 = __builtin_amdgcn_fdot2(xv[k], wr[c + 4][k], s1, false);
+        }
+        acc0[c] = s0;
+        acc1[c] = s1;
+      }
+      const uint32_t off = (uint32_t)((4 * q + j) * a.M + ch0) * 2;
+      h4 s00 = {0, 0, 0, 0}, s01 = s00, s10 = s00, s11 = s00;
+      const int64_t pix = ((int64_t)n * a.Hp + h + 1) * a.Wp + x0 + 1 + 4 * q + j;
+      if (live && x0 + 4 * q + j < a.W) {
+        if (a.epi.skip0) {
+          const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip0) + pix * a.M + ch0;
+          s00 = *reinterpret_cast<const h4*>(sp);
+          s01 = *reinterpret_cast<const h4*>(sp + 4);
+        }
+        if (a.epi.skip1) {
+          const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip1) + pix * a.M + ch0;
+          s10 = *reinterpret_cast<const h4*>(sp);
+          s11 = *reinterpret_cast<const h4*>(sp + 4);
+        }
+      }
+      h4 r0, r1;
+      if (a.epi.act == kActRelu) {
+        r0 = fast4<kActRelu>(acc0, b0, s00, s10);
+        r1 = fast4<kActRelu>(acc1, b1, s01, s11);
+      } else if (a.epi.act == kActSilu) {
+        r0 = fast4<kActSilu>(acc0, b0, s00, s10);
+        r1 = fast4<kActSilu>(acc1, b1, s01, s11);
+      } else {
+        r0 = fast4<kActNone>(acc0, b0, s00, s10);
+        r1 = fast4<kActNone>(acc1, b1, s01, s11);
+      }
+      const h8 rv = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, rv), rs,
+                                             live ? off : 0x80000000u, 0, kNonTemporal);
+    }
+    if (it + 1 < end) {
+      store_item(buf ^ 1);
+      if (it + 2 < end) load_item(it + 2);
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Elementwise, DepthToSpace and boundary IO (off the fused hot path)
 // ---------------------------------------------------------------------------
@@ -1583,6 +1739,26 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
   if (blocks < 1) blocks = 1;
   const bool fast = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && (a.M % 8) == 0 &&
                     !a.epi.do_clip;
+  if (fast && a.g8 <= 16) {
+    const int seg = 4 * 256 / a.g8;
+    const int n_seg = (a.W + seg - 1) / seg;
+    const int64_t items = (int64_t)a.N * a.H * n_seg;
+    if (items < ((int64_t)1 << 31)) {
+      const FastDiv fs = make_fastdiv((uint32_t)n_seg), fh = make_fastdiv((uint32_t)a.H);
+      int64_t grid = (int64_t)cu_count() * 8;  // 8 workgroups per CU (vs 4: 81 -> 76 us)
+      if (grid > items) grid = items;
+      grid = (grid + 7) / 8 * 8;
+      const dim3 gd((unsigned)grid), bd(256);
+      switch (a.g8) {
+        case 1: hipLaunchKernelGGL(direct_conv_c1_rows<1>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
+        case 2: hipLaunchKernelGGL(direct_conv_c1_rows<2>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
+        case 4: hipLaunchKernelGGL(direct_conv_c1_rows<4>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
+        case 8: hipLaunchKernelGGL(direct_conv_c1_rows<8>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
+        default: hipLaunchKernelGGL(direct_conv_c1_rows<16>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
+      }
+      return hipGetLastError();
+    }
+  }
   if (fast)
     hipLaunchKernelGGL(direct_conv_c1<true>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
   else
