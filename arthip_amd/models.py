@@ -217,3 +217,38 @@ def work_per_frame(spec: ModelSpec, n: int, h: int, w: int) -> dict:
         fw += f * (16.0 / 36.0) if cin > 1 else f
         byts += 2.0 * px * (cin + cout * (1 + nskip)) + 2.0 * 9 * cin * cout
     return {"flops_direct": fd, "flops_wino": fw, "bytes": byts}
+
+
+def widen_to_fp32(spec: ModelSpec, name: str | None = None) -> ModelSpec:
+    """The same network as an all-fp32 ONNX model: fp32 initializers (exact
+    widenings of the fp16 weights), fp32 graph IO and no Cast nodes.
+
+    This is the form the reference's VapourSynth plugin converts to fp16 before
+    building (``fp16=1``; convert_float_to_float16.cpp:294-611). The engine
+    takes it directly: weights are rounded to fp16 when they are packed and the
+    boundary converts fp32 <-> fp16, so an fp32 model runs exactly the fp16
+    network with fp32 IO."""
+    g = spec.model.graph
+    boundary = {n.outputs[0]: n.inputs[0] for n in g.nodes if n.op_type == "Cast"}
+    nodes = []
+    for n in g.nodes:
+        if n.op_type == "Cast":
+            continue
+        ins = ["x" if boundary.get(i) == "x" else i for i in n.inputs]
+        nodes.append(op.Node(n.op_type, ins, list(n.outputs), n.name, n.domain, list(n.attributes)))
+    out_name = g.outputs[0].name
+    if out_name in boundary:  # the graph output was a Cast of `src`
+        src = boundary[out_name]
+        for n in nodes:
+            n.outputs = [out_name if o == src else o for o in n.outputs]
+    inits = []
+    for t in g.initializers:
+        a = t.to_numpy()
+        inits.append(op.tensor(t.name, a.astype(np.float32) if a.dtype == np.float16 else a))
+    gi, go = g.inputs[0], g.outputs[0]
+    graph = op.Graph(nodes=nodes, name=g.name, initializers=inits,
+                     inputs=[op.value_info(gi.name, op.FLOAT, gi.shape)],
+                     outputs=[op.value_info(go.name, op.FLOAT, go.shape)])
+    model = op.Model(graph=graph, opset_imports=list(spec.model.opset_imports))
+    return ModelSpec(model, name or spec.name + "_fp32", spec.in_channels, spec.out_channels,
+                     spec.scale, list(spec.convs), list(spec.skips_per_conv))

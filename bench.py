@@ -14,6 +14,10 @@ Extra objects in the line:
                 the launch stream during the timed steps; against 8 TB/s HBM peak.
                 traffic: HBM bytes per launch from the committed rocprofv3
                 FETCH_SIZE/WRITE_SIZE summary (profiles/), when present.
+                stream_copy_gbs: achievable HBM bandwidth on this device, a plain
+                device copy (torch copy_) of one activation-sized buffer
+                (265 MB read + 265 MB written), for reading `achieved` against
+                what a streaming kernel reaches rather than only the 8 TB/s peak.
   cpu_baseline  the CPU oracle (oracle/, plain C + OpenMP, fp32 math with fp16
                 storage between nodes) on a bounded band of the same frame on the
                 host's cores, scaled to frames/s.
@@ -92,6 +96,27 @@ def cpu_baseline(spec, x_full, rows: int) -> dict | None:
                    f"{dt:.1f} s), C oracle fp32 math + fp16 storage per node, OpenMP; "
                    f"frames/s = band fraction / time"),
     }
+
+
+def stream_copy_gbs(nbytes: int, reps: int = 20) -> float:
+    """Read + write GB/s of a device-to-device copy of nbytes (best of reps)."""
+    import torch
+    n = nbytes // 2
+    a = torch.ones(n, dtype=torch.float16, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        b.copy_(a)
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) / 1000.0)
+    del a, b
+    return 2.0 * n * 2 / best / 1e9
 
 
 def traffic_from_profiles(kernel_key: str):
@@ -187,6 +212,7 @@ def main() -> int:
         if dom_launches:
             mean_s = dom_ms / 1000.0 / dom_launches
             achieved = dom_bytes / dom_launches / mean_s / 1e9
+            copy_gbs = stream_copy_gbs(2 * px * 64)
             roofline = {
                 "bound": "hbm",
                 "kernel": "winograd_conv (F(2x2,3x3), C=M=%d)" % spec.convs[1][0],
@@ -200,6 +226,8 @@ def main() -> int:
                 "alg_bytes_per_launch": round(dom_bytes / dom_launches),
                 "mfma_frac_direct_equiv": round(dom_flops / dom_launches / mean_s / 1e12
                                                 / MFMA_FP16_PEAK_TFLOPS, 4),
+                "stream_copy_gbs": round(copy_gbs, 1),
+                "frac_of_stream_copy": round(achieved / copy_gbs, 4),
             }
 
     cpu = cpu_baseline(spec, x_host, min(args.cpu_rows, h)) if args.cpu_rows else None

@@ -93,3 +93,16 @@ def test_fp32_io_is_detected(fixtures):
     e = Engine(0).build(models.r8f64(io_fp32=True))
     assert e.io_info()[:2] == (True, True)
     assert len(ops_of(e)) == 18
+
+
+@pytest.mark.parametrize("builder", [models.c4f32, models.r8f64, models.shipped_like])
+def test_fp32_model_fuses_like_fp16(builder):
+    """The all-fp32 form of a model (what the reference's plugin converts with
+    fp16=1) builds with fp32 IO and lowers to the same fused ops."""
+    spec = builder(seed=0)
+    wide = models.widen_to_fp32(spec)
+    e16, e32 = Engine(0).build(spec), Engine(0).build(wide)
+    assert e32.io_info()[:2] == (True, True)
+    assert e16.io_info()[2:] == e32.io_info()[2:]
+    ops = lambda d: [l.split(":")[0].split(" ", 1)[1] for l in d.splitlines() if l.startswith("op")]
+    assert ops(e16.describe()) == ops(e32.describe())

@@ -158,3 +158,30 @@ def test_shipped_model_on_real_image_meets_gate():
     print("shipped luma 256x256", s)
     assert got.shape == (1, 1, 512, 512)
     assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
+
+
+@pytest.mark.parametrize("builder,hw", [(models.c4f32, (36, 52)), (models.r8f64, (24, 40)),
+                                        (models.shipped_like, (20, 36))])
+def test_fp32_model_runs_the_fp16_network(builder, hw):
+    """An all-fp32 model (fp32 initializers and IO, no Casts) runs exactly the
+    fp16 network: against the fp16 model on the same (fp16-representable)
+    input, the fp32 output is the fp16 output before its final rounding, so the
+    two differ by at most half an fp16 ulp; and it is within the same bound of
+    the oracle on the fp16 model as the fp16 engine output is."""
+    spec = builder(seed=0)
+    wide = models.widen_to_fp32(spec)
+    h, w = hw
+    x16 = models.synthetic_input((1, spec.in_channels, h, w), seed=3)
+    with Engine(0) as e16, Engine(0) as e32:
+        e16.build(spec)
+        e32.build(wide)
+        assert e32.io_info()[:2] == (True, True)
+        y16 = e16.run(x16).astype(np.float64)
+        y32 = e32.run(x16.astype(np.float32)).astype(np.float64)
+    assert y32.shape == y16.shape
+    half_ulp = np.spacing(np.abs(y16).astype(np.float16)).astype(np.float64) / 2
+    assert np.all(np.abs(y32 - y16) <= half_ulp), float(np.abs(y32 - y16).max())
+    want = run_model(spec.model, x16)
+    s16, s32 = _compare(y16, want), _compare(y32, want)
+    print(spec.name, "fp16 model", s16, "fp32 model", s32)
+    assert s32["rel_rms"] <= s16["rel_rms"] * 1.05 + 1e-6
