@@ -214,3 +214,22 @@ def test_strip_long_runs():
     # and most ranges cross a strip boundary.
     x, wt, b = make_case(16, 1, 64, 64, 360, 640)
     check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), "strip 360x640")
+
+
+# Degenerate sizes: one tile row / column, a single pixel, widths below one
+# strip (32 px) or one head-conv segment (128 px at M = 64).
+TINY = [(1, 1), (1, 5), (2, 2), (3, 1), (1, 64), (5, 3), (2, 33)]
+
+
+@pytest.mark.parametrize("h,w", TINY)
+def test_strip_tiny(h, w):
+    x, wt, b = make_case(20, 1, 64, 64, h, w)
+    rng = np.random.default_rng(21)
+    skips = [rng.standard_normal((1, 64, h, w)).astype(np.float16)]
+    check(run_conv(x, wt, b, 1, skips), oracle_conv(x, wt, b, 1, skips), f"strip64 {h}x{w}")
+
+
+@pytest.mark.parametrize("h,w", TINY)
+def test_head_tiny(h, w):
+    x, wt, b = make_case(22, 2, 1, 64, h, w)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), f"head {h}x{w}")

@@ -185,3 +185,23 @@ def test_fp32_model_runs_the_fp16_network(builder, hw):
     s16, s32 = _compare(y16, want), _compare(y32, want)
     print(spec.name, "fp16 model", s16, "fp32 model", s32)
     assert s32["rel_rms"] <= s16["rel_rms"] * 1.05 + 1e-6
+
+
+@pytest.mark.parametrize("builder,hw", [(models.r8f64, (1, 1)), (models.r8f64, (3, 5)),
+                                        (models.r8f64, (2, 65)), (models.c4f32, (1, 3)),
+                                        (models.c4f32, (7, 130)), (models.shipped_like, (5, 2))])
+def test_tiny_frames(builder, hw):
+    """Whole models (head, strip body, narrow tail with DepthToSpace) on frames
+    of a few pixels: every kernel's edge handling at once."""
+    spec = builder(seed=0)
+    h, w = hw
+    x = models.synthetic_input((1, spec.in_channels, h, w), seed=4)
+    with Engine(0) as e:
+        got = e.build(spec).run(x).astype(np.float32)
+    want = run_model(spec.model, x)
+    floor = run_model(spec.model, x, round_fp16=False)
+    s, f = _compare(got, want), _compare(floor, want)
+    print(spec.name, hw, s, "floor", f)
+    assert got.shape == want.shape
+    assert np.isfinite(got).all()
+    assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
