@@ -835,6 +835,277 @@ winograd_strip(StripArgs a) {
   store_phase(last_buf);
 }
 
+// fp16 rounding and activation of 4 channels whose accumulator holds the bias.
+template <int ACT>
+__device__ __forceinline__ h4 strip_act4(f4 y) {
+  h4 r = to_h4(y);
+  if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
+  if (ACT == kActSilu) {
+    f4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = (float)r[e];
+      t[e] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    }
+    r = to_h4(t);
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Producer/consumer strip conv (C = M = 64, no residual inputs)
+// ---------------------------------------------------------------------------
+//
+// The items, V' layout, fold and output staging of winograd_strip, split over
+// two kinds of waves of one 512-thread workgroup per CU:
+//   * waves 0-3 (consumers) keep U' of 16 output channels each in VGPRs and
+//     only run the MFMA fold and the activation into staging;
+//   * waves 4-7 (producers) load input rows, write V' and move staged outputs
+//     to HBM. Holding no U', they keep PIPE_ROWS - 1 row pairs in flight ahead
+//     of the transform, so HBM latency hides behind that many items of work.
+// Step j (one barrier each): the producers store item j-2 and transform item
+// j, the consumers fold item j-1. V' and staging are double-buffered by item
+// parity, so each buffer's writes and reads are a barrier apart. A run (the
+// items of one strip) restarts the producers' row window.
+constexpr int PIPE_ROWS = 6;
+
+template <int ACT>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+winograd_pipe(StripArgs a) {
+  constexpr int KC = 2;
+  constexpr int C = 32 * KC;
+  constexpr int NCW = 2 * KC;  // consumer waves
+  constexpr int NW = PIPE_ROWS;
+  constexpr int WPS = StripLds<KC>::WPS;
+  constexpr int VBUF = StripLds<KC>::VBUF;
+  constexpr int SBUF = StripStage<KC>::SBUF;
+  constexpr int GR = StripStage<KC>::G;
+  constexpr int QUADS = C / 4;
+  constexpr int PX = 2 * C;
+  extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];  // 2 V' + 2 staging buffers
+  _Float16* const stg = vlds + 2 * VBUF;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+
+  const int G = gridDim.x;
+  const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int begin = (int)((int64_t)a.n_items * slot / G);
+  const int end = (int)((int64_t)a.n_items * (slot + 1) / G);
+  if (begin >= end) return;  // uniform across the workgroup
+  const int K = end - begin;
+
+  if (wave < NCW) {
+    // ---- consumers: steps 1..K fold items 0..K-1 --------------------------
+    h8 u[16][KC];
+    {
+      const h8* up = reinterpret_cast<const h8*>(a.u) + (size_t)wave * (16 * KC * 64) + lane;
+#pragma unroll
+      for (int p = 0; p < 16; ++p)
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) u[p][kc] = up[(p * KC + kc) * 64];
+    }
+    const int tcol = lane & 15;
+    const int kq = lane >> 4;
+    const int ch0 = 16 * wave + 4 * kq;
+    const f4 bias4 = *reinterpret_cast<const f4*>(a.bias + ch0);
+    const _Float16* vr0[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) vr0[kc] = vlds + StripLds<KC>::at(tcol, 32 * kc + 8 * kq);
+    const int sw0 = StripStage<KC>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
+
+    auto fold = [&](auto buf_tag) {
+      constexpr int BUF = decltype(buf_tag)::value;
+      auto mm = [&](int p, f4 acc) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              u[p][kc], *reinterpret_cast<const h8*>(vr0[kc] + BUF * VBUF + p * WPS), acc, 0, 0,
+              0);
+        return acc;
+      };
+      const f4 z = {0, 0, 0, 0};
+      const f4 m2 = {-2.0f, -2.0f, -2.0f, -2.0f};
+      f4 y00, y01, y10, y11;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f4 P, Q;
+        if (r == 1) {
+          const f4 Y = mm(5, bias4);
+          const f4 b = mm(6, Y);
+          P = mm(4, b);
+          const f4 c = mm(7, Y);
+          Q = (c - b) + Y;
+        } else {
+          const f4 X = mm(4 * r + 2, z);
+          const f4 b = mm(4 * r + 1, X);
+          P = mm(4 * r, b);
+          const f4 c = mm(4 * r + 3, b);
+          Q = __builtin_elementwise_fma(X, m2, c);
+        }
+        if (r == 0) {
+          y00 = P;
+          y01 = Q;
+        } else if (r == 1) {
+          y00 += P;
+          y01 += Q;
+          y10 = P;
+          y11 = Q;
+        } else if (r == 2) {
+          y00 += P;
+          y01 += Q;
+          y10 -= P;
+          y11 -= Q;
+        } else {
+          y10 -= P;
+          y11 -= Q;
+        }
+      }
+      _Float16* sw = stg + BUF * SBUF + sw0;
+      *reinterpret_cast<h4*>(sw) = strip_act4<ACT>(y00);
+      *reinterpret_cast<h4*>(sw + C) = strip_act4<ACT>(y01);
+      *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<ACT>(y10);
+      *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<ACT>(y11);
+    };
+
+    lds_sync();  // step 0
+    for (int j = 0;;) {
+      fold(IntC<0>{});
+      lds_sync();
+      if (++j == K) break;
+      fold(IntC<1>{});
+      lds_sync();
+      if (++j == K) break;
+    }
+    lds_sync();  // step K + 1
+    return;
+  }
+
+  // ---- producers: step j stores item j-2 and transforms item j -------------
+  const int ptid = tid - 64 * NCW;
+  const int tt = ptid / QUADS;
+  const int tq = ptid - tt * QUADS;
+  _Float16* const vw0 = vlds + StripLds<KC>::at(tt, 4 * tq);
+  const int sx = ptid / GR;
+  const int sg = ptid - sx * GR;
+  const int sr0 = StripStage<KC>::at(0, sx, sg);
+  const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
+  const int64_t row_bytes = (int64_t)a.Wp * PX;
+  const uint32_t rb32 = (uint32_t)row_bytes;
+  const int n_rec = (int)(rb32 + 32 * PX);
+  constexpr uint32_t kOob = 0x80000000u;
+
+  int n, s, th;
+  auto decode = [&](int item) {
+    const uint32_t sgl = fdiv((uint32_t)item, a.fd_tiles_h);
+    th = item - (int)(sgl * (uint32_t)a.tiles_h);
+    const uint32_t nn = fdiv(sgl, a.fd_strips);
+    s = (int)(sgl - nn * (uint32_t)a.n_strips);
+    n = (int)nn;
+  };
+  uint32_t in_lane = 0;
+  auto in_row = [&](int r) {
+    if (r > a.Hp - 2) r = a.Hp - 2;
+    return reinterpret_cast<const char*>(a.in) + (((int64_t)n * a.Hp + r) * a.Wp + 32 * s) * PX;
+  };
+  auto load2 = [&](h2 (&x)[16], const char* rb) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h4 v = *reinterpret_cast<const h4*>(rb + r * row_bytes + in_lane + j * PX);
+        x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
+        x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
+      }
+  };
+
+  // Items j-1 (q1) and j-2 (q2) of step j; every step issues the same two
+  // stores (out-of-range offsets for an absent item or pixels past the edge).
+  int q1n = 0, q1s = 0, q1t = 0, q2n = 0, q2s = 0, q2t = 0;
+  bool q1v = false, q2v = false;
+  int par = 0;  // parity of step j (= parity of items j and j-2)
+  auto store_step = [&]() {
+    const int64_t pix0 = ((int64_t)q2n * a.Hp + 2 * q2t + 1) * a.Wp + 32 * q2s + 1;
+    char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, n_rec, 0x00020000);
+    const _Float16* sp = stg + par * SBUF + sr0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const h8 v = *reinterpret_cast<const h8*>(sp + r * 32 * C);
+      const bool ok = q2v && (32 * q2s + sx < a.W) && (r == 0 || 2 * q2t + 1 < a.H);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs,
+                                             ok ? (uint32_t)r * rb32 + s_lane : kOob, 0,
+                                             kNonTemporal);
+    }
+    q2n = q1n;
+    q2s = q1s;
+    q2t = q1t;
+    q2v = q1v;
+  };
+  auto step = [&](h2 (&top)[16], h2 (&bot)[16]) {
+    store_step();
+    strip_transform<KC>(vw0 + par * VBUF, top, bot);
+    load2(top, in_row(2 * (th + NW)));
+    q1n = n;
+    q1s = s;
+    q1t = th;
+    q1v = true;
+    ++th;
+    par ^= 1;
+    lds_sync();
+  };
+
+  h2 W0[16], W1[16], W2[16], W3[16], W4[16], W5[16];
+  static_assert(NW == 6, "row window slots");
+  for (int it = begin; it < end;) {
+    decode(it);
+    const int len = min(end - it, a.tiles_h - th);
+    {
+      const int t = (16 * s + tt < a.tiles_w) ? tt : 0;
+      in_lane = (uint32_t)(2 * t * C + 4 * tq) * 2;
+    }
+    load2(W0, in_row(2 * th));
+    load2(W1, in_row(2 * th + 2));
+    load2(W2, in_row(2 * th + 4));
+    load2(W3, in_row(2 * th + 6));
+    load2(W4, in_row(2 * th + 8));
+    load2(W5, in_row(2 * th + 10));
+    // Whole cycles of the six slots, then the remainder. A loop with one
+    // exit keeps the compiler's count of outstanding loads exact at the loop
+    // head (a break after every step would merge all six states there and
+    // force near-complete waits).
+    int k = len;
+    for (; k >= NW; k -= NW) {
+      step(W0, W1);
+      step(W1, W2);
+      step(W2, W3);
+      step(W3, W4);
+      step(W4, W5);
+      step(W5, W0);
+    }
+    if (k > 0) {
+      step(W0, W1);
+      if (k > 1) {
+        step(W1, W2);
+        if (k > 2) {
+          step(W2, W3);
+          if (k > 3) {
+            step(W3, W4);
+            if (k > 4) step(W4, W5);
+          }
+        }
+      }
+    }
+    it += len;
+  }
+  store_step();  // step K: item K-2
+  par ^= 1;
+  lds_sync();
+  store_step();  // step K+1: item K-1
+  lds_sync();
+}
+
 __device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
 }
@@ -1582,6 +1853,20 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
   a.fd_tiles_h = make_fastdiv((uint32_t)a.tiles_h);
   a.fd_strips = make_fastdiv((uint32_t)a.n_strips);
   const int kc = w.C / 32;
+  if (kc == 2 && nskip == 0) {
+    StripKernel pf = w.epi.act == kActRelu   ? winograd_pipe<kActRelu>
+                     : w.epi.act == kActSilu ? winograd_pipe<kActSilu>
+                                             : winograd_pipe<kActNone>;
+    const size_t lds = (size_t)2 * (StripLds<2>::VBUF + StripStage<2>::SBUF) * 2;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    int64_t grid = cu_count();
+    if (grid > items) grid = items;
+    grid = (grid + 7) / 8 * 8;
+    hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(512), lds, s, a);
+    return hipGetLastError();
+  }
   StripKernel fn = kc == 1 ? strip_kernel_act<1>(w.epi.act, nskip)
                            : strip_kernel_act<2>(w.epi.act, nskip);
   if (fn == nullptr) return hipErrorInvalidValue;
