@@ -499,10 +499,11 @@ struct StripLds {
 // ReLU layers by 2 us but costs the residual layers 16 us, so those stay plain.
 constexpr int kNonTemporal = 2;
 
-template <int KC>
-__device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16],
-                                                const h2 (&bot)[16]) {
-  constexpr int WPS = StripLds<KC>::WPS;
+// V' of one (tile, 4-channel) task from its 4x4 patch (rows 0-1 in top, 2-3
+// in bot), written to LDS at vw + position * WPS.
+template <int WPS>
+__device__ __forceinline__ void v_transform(_Float16* vw, const h2 (&top)[16],
+                                            const h2 (&bot)[16]) {
   const h2 qp = {0.25f16, 0.25f16};
   const h2 qn = {-0.25f16, -0.25f16};
   h2 t[4][4][2];
@@ -536,9 +537,15 @@ __device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16
   }
 }
 
-// Fast epilogue of 4 channels whose accumulator already holds the bias.
+template <int KC>
+__device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16],
+                                                const h2 (&bot)[16]) {
+  v_transform<StripLds<KC>::WPS>(vw, top, bot);
+}
+
+// fp16 rounding and activation of 4 channels whose accumulator holds the bias.
 template <int ACT>
-__device__ __forceinline__ h4 strip_epi4(f4 y, h4 s0, h4 s1) {
+__device__ __forceinline__ h4 strip_act4(f4 y) {
   h4 r = to_h4(y);
   if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
   if (ACT == kActSilu) {
@@ -550,8 +557,6 @@ __device__ __forceinline__ h4 strip_epi4(f4 y, h4 s0, h4 s1) {
     }
     r = to_h4(t);
   }
-  r += s0;
-  r += s1;
   return r;
 }
 
@@ -711,8 +716,8 @@ winograd_strip(StripArgs a) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C);
-      v += skr[0][r];
-      v += skr[1][r];
+      if (NSKIP > 0) v += skr[0][r];
+      if (NSKIP > 1) v += skr[1][r];
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs, st_off(r), 0,
                                              kNonTemporal);
     }
@@ -787,12 +792,11 @@ winograd_strip(StripArgs a) {
       }
     }
     store_phase(BUF ^ 1);
-    const h4 zh = {0, 0, 0, 0};
     _Float16* sw = stg + BUF * SBUF + sw0;
-    *reinterpret_cast<h4*>(sw) = strip_epi4<ACT>(y00, zh, zh);
-    *reinterpret_cast<h4*>(sw + C) = strip_epi4<ACT>(y01, zh, zh);
-    *reinterpret_cast<h4*>(sw + 32 * C) = strip_epi4<ACT>(y10, zh, zh);
-    *reinterpret_cast<h4*>(sw + 33 * C) = strip_epi4<ACT>(y11, zh, zh);
+    *reinterpret_cast<h4*>(sw) = strip_act4<ACT>(y00);
+    *reinterpret_cast<h4*>(sw + C) = strip_act4<ACT>(y01);
+    *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<ACT>(y10);
+    *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<ACT>(y11);
     pn = n;
     ps = s;
     pth = th;
@@ -835,39 +839,48 @@ winograd_strip(StripArgs a) {
   store_phase(last_buf);
 }
 
-// fp16 rounding and activation of 4 channels whose accumulator holds the bias.
-template <int ACT>
-__device__ __forceinline__ h4 strip_act4(f4 y) {
-  h4 r = to_h4(y);
-  if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
-  if (ACT == kActSilu) {
-    f4 t;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x = (float)r[e];
-      t[e] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
-    }
-    r = to_h4(t);
-  }
-  return r;
-}
-
 // ---------------------------------------------------------------------------
 // Producer/consumer strip conv (C = M = 64, no residual inputs)
 // ---------------------------------------------------------------------------
 //
-// The items, V' layout, fold and output staging of winograd_strip, split over
-// two kinds of waves of one 512-thread workgroup per CU:
-//   * waves 0-3 (consumers) keep U' of 16 output channels each in VGPRs and
-//     only run the MFMA fold and the activation into staging;
-//   * waves 4-7 (producers) load input rows, write V' and move staged outputs
-//     to HBM. Holding no U', they keep PIPE_ROWS - 1 row pairs in flight ahead
-//     of the transform, so HBM latency hides behind that many items of work.
-// Step j (one barrier each): the producers store item j-2 and transform item
-// j, the consumers fold item j-1. V' and staging are double-buffered by item
+// The items (1 tile row x 16 tiles), fold and output staging of
+// winograd_strip, split over two kinds of waves of one 512-thread workgroup
+// per CU:
+//   * waves 0-3 (consumers) keep U' of 16 output channels each in VGPRs, run
+//     the MFMA fold and the activation into staging, and move the staged
+//     outputs of the item before to HBM;
+//   * waves 4-7 (producers) load input rows and write V'. Holding no U', they
+//     keep PIPE_ROWS - 1 row pairs in flight ahead of the transform, so HBM
+//     latency hides behind that many items of work.
+// Step j (one barrier each): the producers transform item j; the consumers
+// store item j-2 and fold item j-1. V' and staging are double-buffered by item
 // parity, so each buffer's writes and reads are a barrier apart. A run (the
 // items of one strip) restarts the producers' row window.
+//
+// Measured on the 1080p 64 -> 64 ReLU conv: 145 us with winograd_strip, 122 us
+// here. Items of 32 tiles (two MFMA column blocks per wave) ran at 146 us: at
+// 256 VGPRs the compiler keeps only one or two B reads ahead of the MFMAs.
+// Splitting the fold by position rows over 8 consumer waves (12 waves, half of
+// U' each, partial sums exchanged through LDS) ran at 137 us.
 constexpr int PIPE_ROWS = 6;
+
+// V' of an item: [position][tile][64 channels], 128-byte tile rows with the
+// channel groups of tile t at g ^ (t & 7) (as StripLds<2>); staging
+// [row][pixel][64 channels] as StripStage<2>.
+struct PipeLds {
+  static constexpr int TILES = 16;
+  static constexpr int PXS = 32;             // pixels per staged row
+  static constexpr int WPS = TILES * 64;     // halfs per position
+  static constexpr int VBUF = 16 * WPS;      // halfs per V' buffer
+  static constexpr int SBUF = 2 * PXS * 64;  // halfs per staging buffer
+  __host__ __device__ static constexpr int at(int t, int c) { return StripLds<2>::at(t, c); }
+  __host__ __device__ static constexpr int st(int row, int x, int g) {
+    return StripStage<2>::at(row, x, g);
+  }
+  static constexpr size_t lds_bytes() { return (size_t)2 * (VBUF + SBUF) * 2; }
+};
+static_assert(PipeLds::WPS == StripLds<2>::WPS && PipeLds::SBUF == StripStage<2>::SBUF,
+              "pipe and strip layouts agree");
 
 template <int ACT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -876,10 +889,11 @@ winograd_pipe(StripArgs a) {
   constexpr int C = 32 * KC;
   constexpr int NCW = 2 * KC;  // consumer waves
   constexpr int NW = PIPE_ROWS;
-  constexpr int WPS = StripLds<KC>::WPS;
-  constexpr int VBUF = StripLds<KC>::VBUF;
-  constexpr int SBUF = StripStage<KC>::SBUF;
-  constexpr int GR = StripStage<KC>::G;
+  using L = PipeLds;
+  constexpr int WPS = L::WPS;
+  constexpr int VBUF = L::VBUF;
+  constexpr int SBUF = L::SBUF;
+  constexpr int PXS = L::PXS;
   constexpr int QUADS = C / 4;
   constexpr int PX = 2 * C;
   extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];  // 2 V' + 2 staging buffers
@@ -895,8 +909,18 @@ winograd_pipe(StripArgs a) {
   if (begin >= end) return;  // uniform across the workgroup
   const int K = end - begin;
 
+  const int64_t row_bytes = (int64_t)a.Wp * PX;
+  int n, s, th;
+  auto decode = [&](int item) {
+    const uint32_t sgl = fdiv((uint32_t)item, a.fd_tiles_h);
+    th = item - (int)(sgl * (uint32_t)a.tiles_h);
+    const uint32_t nn = fdiv(sgl, a.fd_strips);
+    s = (int)(sgl - nn * (uint32_t)a.n_strips);
+    n = (int)nn;
+  };
+
   if (wave < NCW) {
-    // ---- consumers: steps 1..K fold items 0..K-1 --------------------------
+    // ---- consumers: step j stores item j-2 and folds item j-1 -------------
     h8 u[16][KC];
     {
       const h8* up = reinterpret_cast<const h8*>(a.u) + (size_t)wave * (16 * KC * 64) + lane;
@@ -911,9 +935,34 @@ winograd_pipe(StripArgs a) {
     const f4 bias4 = *reinterpret_cast<const f4*>(a.bias + ch0);
     const _Float16* vr0[KC];
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) vr0[kc] = vlds + StripLds<KC>::at(tcol, 32 * kc + 8 * kq);
-    const int sw0 = StripStage<KC>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
+    for (int kc = 0; kc < KC; ++kc) vr0[kc] = vlds + L::at(tcol, 32 * kc + 8 * kq);
+    const int sw0 = L::st(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
+    // Store mapping: thread handles 16-byte group sg of pixel sx in both rows.
+    const int sx = tid >> 3;
+    const int sg = tid & 7;
+    const int sr0 = L::st(0, sx, sg);
+    const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
+    const uint32_t rb32 = (uint32_t)row_bytes;
+    const int n_rec = (int)(rb32 + PXS * PX);
+    constexpr uint32_t kOob = 0x80000000u;
 
+    // Item `item` from staging buffer SB; absent items and pixels past the
+    // edges get out-of-range offsets, so every step issues the same two stores.
+    auto store_item = [&](int item, bool live, int SB) {
+      decode(item);
+      const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + PXS * s + 1;
+      char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, n_rec, 0x00020000);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * PXS * C);
+        const bool ok = live && (PXS * s + sx < a.W) && (r == 0 || 2 * th + 1 < a.H);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs,
+                                               ok ? (uint32_t)r * rb32 + s_lane : kOob, 0,
+                                               kNonTemporal);
+      }
+    };
     auto fold = [&](auto buf_tag) {
       constexpr int BUF = decltype(buf_tag)::value;
       auto mm = [&](int p, f4 acc) {
@@ -964,49 +1013,38 @@ winograd_pipe(StripArgs a) {
       _Float16* sw = stg + BUF * SBUF + sw0;
       *reinterpret_cast<h4*>(sw) = strip_act4<ACT>(y00);
       *reinterpret_cast<h4*>(sw + C) = strip_act4<ACT>(y01);
-      *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<ACT>(y10);
-      *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<ACT>(y11);
+      *reinterpret_cast<h4*>(sw + PXS * C) = strip_act4<ACT>(y10);
+      *reinterpret_cast<h4*>(sw + (PXS + 1) * C) = strip_act4<ACT>(y11);
     };
 
+    // Step j folds item j-1 into buffer (j-1)&1 and stores item j-2 from
+    // buffer j&1. Steps alternate odd/even so both parities are static.
     lds_sync();  // step 0
-    for (int j = 0;;) {
+    for (int j = 1;; ++j) {
+      store_item(begin + (j >= 2 ? j - 2 : 0), j >= 2, 1);  // odd j
       fold(IntC<0>{});
       lds_sync();
-      if (++j == K) break;
+      if (j == K) break;
+      ++j;
+      store_item(begin + j - 2, true, 0);  // even j
       fold(IntC<1>{});
       lds_sync();
-      if (++j == K) break;
+      if (j == K) break;
     }
-    lds_sync();  // step K + 1
+    store_item(begin + K - 1, true, (K + 1) & 1);  // step K + 1
+    lds_sync();
     return;
   }
 
-  // ---- producers: step j stores item j-2 and transforms item j -------------
+  // ---- producers: step j transforms item j ---------------------------------
   const int ptid = tid - 64 * NCW;
   const int tt = ptid / QUADS;
   const int tq = ptid - tt * QUADS;
-  _Float16* const vw0 = vlds + StripLds<KC>::at(tt, 4 * tq);
-  const int sx = ptid / GR;
-  const int sg = ptid - sx * GR;
-  const int sr0 = StripStage<KC>::at(0, sx, sg);
-  const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
-  const int64_t row_bytes = (int64_t)a.Wp * PX;
-  const uint32_t rb32 = (uint32_t)row_bytes;
-  const int n_rec = (int)(rb32 + 32 * PX);
-  constexpr uint32_t kOob = 0x80000000u;
-
-  int n, s, th;
-  auto decode = [&](int item) {
-    const uint32_t sgl = fdiv((uint32_t)item, a.fd_tiles_h);
-    th = item - (int)(sgl * (uint32_t)a.tiles_h);
-    const uint32_t nn = fdiv(sgl, a.fd_strips);
-    s = (int)(sgl - nn * (uint32_t)a.n_strips);
-    n = (int)nn;
-  };
+  _Float16* const vw0 = vlds + L::at(tt, 4 * tq);
   uint32_t in_lane = 0;
   auto in_row = [&](int r) {
     if (r > a.Hp - 2) r = a.Hp - 2;
-    return reinterpret_cast<const char*>(a.in) + (((int64_t)n * a.Hp + r) * a.Wp + 32 * s) * PX;
+    return reinterpret_cast<const char*>(a.in) + (((int64_t)n * a.Hp + r) * a.Wp + PXS * s) * PX;
   };
   auto load2 = [&](h2 (&x)[16], const char* rb) {
 #pragma unroll
@@ -1018,92 +1056,49 @@ winograd_pipe(StripArgs a) {
         x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
       }
   };
-
-  // Items j-1 (q1) and j-2 (q2) of step j; every step issues the same two
-  // stores (out-of-range offsets for an absent item or pixels past the edge).
-  int q1n = 0, q1s = 0, q1t = 0, q2n = 0, q2s = 0, q2t = 0;
-  bool q1v = false, q2v = false;
-  int par = 0;  // parity of step j (= parity of items j and j-2)
-  auto store_step = [&]() {
-    const int64_t pix0 = ((int64_t)q2n * a.Hp + 2 * q2t + 1) * a.Wp + 32 * q2s + 1;
-    char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, n_rec, 0x00020000);
-    const _Float16* sp = stg + par * SBUF + sr0;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const h8 v = *reinterpret_cast<const h8*>(sp + r * 32 * C);
-      const bool ok = q2v && (32 * q2s + sx < a.W) && (r == 0 || 2 * q2t + 1 < a.H);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs,
-                                             ok ? (uint32_t)r * rb32 + s_lane : kOob, 0,
-                                             kNonTemporal);
-    }
-    q2n = q1n;
-    q2s = q1s;
-    q2t = q1t;
-    q2v = q1v;
-  };
+  int par = 0;  // parity of step j = parity of item j
   auto step = [&](h2 (&top)[16], h2 (&bot)[16]) {
-    store_step();
-    strip_transform<KC>(vw0 + par * VBUF, top, bot);
+    v_transform<WPS>(vw0 + par * VBUF, top, bot);
     load2(top, in_row(2 * (th + NW)));
-    q1n = n;
-    q1s = s;
-    q1t = th;
-    q1v = true;
     ++th;
     par ^= 1;
     lds_sync();
   };
 
-  h2 W0[16], W1[16], W2[16], W3[16], W4[16], W5[16];
-  static_assert(NW == 6, "row window slots");
+  h2 W[NW][16];
   for (int it = begin; it < end;) {
     decode(it);
     const int len = min(end - it, a.tiles_h - th);
     {
-      const int t = (16 * s + tt < a.tiles_w) ? tt : 0;
+      // Tiles past the right edge read tile 0's patch (never stored).
+      const int t = (L::TILES * s + tt < a.tiles_w) ? tt : 0;
       in_lane = (uint32_t)(2 * t * C + 4 * tq) * 2;
     }
-    load2(W0, in_row(2 * th));
-    load2(W1, in_row(2 * th + 2));
-    load2(W2, in_row(2 * th + 4));
-    load2(W3, in_row(2 * th + 6));
-    load2(W4, in_row(2 * th + 8));
-    load2(W5, in_row(2 * th + 10));
-    // Whole cycles of the six slots, then the remainder. A loop with one
-    // exit keeps the compiler's count of outstanding loads exact at the loop
-    // head (a break after every step would merge all six states there and
-    // force near-complete waits).
+#pragma unroll
+    for (int m = 0; m < NW; ++m) load2(W[m], in_row(2 * (th + m)));
+    // Whole cycles of the slots, then the remainder as nested conditions. A
+    // loop with one exit keeps the compiler's count of outstanding loads exact
+    // at the loop head (a break after every step would merge all the step
+    // states there and force near-complete waits).
     int k = len;
     for (; k >= NW; k -= NW) {
-      step(W0, W1);
-      step(W1, W2);
-      step(W2, W3);
-      step(W3, W4);
-      step(W4, W5);
-      step(W5, W0);
+#pragma unroll
+      for (int m = 0; m < NW; ++m) step(W[m], W[(m + 1) % NW]);
     }
-    if (k > 0) {
-      step(W0, W1);
-      if (k > 1) {
-        step(W1, W2);
-        if (k > 2) {
-          step(W2, W3);
-          if (k > 3) {
-            step(W3, W4);
-            if (k > 4) step(W4, W5);
-          }
+    auto rest = [&](auto self, auto m_tag) {
+      constexpr int M = decltype(m_tag)::value;
+      if constexpr (M < NW - 1) {
+        if (k > M) {
+          step(W[M], W[M + 1]);
+          self(self, IntC<M + 1>{});
         }
       }
-    }
+    };
+    rest(rest, IntC<0>{});
     it += len;
   }
-  store_step();  // step K: item K-2
-  par ^= 1;
-  lds_sync();
-  store_step();  // step K+1: item K-1
-  lds_sync();
+  lds_sync();  // step K
+  lds_sync();  // step K + 1
 }
 
 __device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
@@ -1857,7 +1852,7 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
     StripKernel pf = w.epi.act == kActRelu   ? winograd_pipe<kActRelu>
                      : w.epi.act == kActSilu ? winograd_pipe<kActSilu>
                                              : winograd_pipe<kActNone>;
-    const size_t lds = (size_t)2 * (StripLds<2>::VBUF + StripStage<2>::SBUF) * 2;
+    const size_t lds = PipeLds::lds_bytes();
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
