@@ -1352,6 +1352,196 @@ conv3x3_narrow(NarrowArgs a) {
   store_item(last_tb, have_prev);
 }
 
+// Tail conv with the three taps of a kernel row packed into one MFMA (M <= 5).
+// B columns are (dx, n) -> dx*M + n, so per kernel row dy and 32-channel chunk
+// one MFMA gives D[x][(dx, n)] = sum_c in[dy][x][c] * w[n][c][dy][dx] for the
+// wave's 16 pixels x; dy and the chunks accumulate in the MFMA, so a wave
+// issues 3 * KC MFMAs per item instead of 9 * KC. The conv output is
+// out[x][n] = D[x][(0,n)] + D[x+1][(1,n)] + D[x+2][(2,n)] (+ bias), summed in
+// the store phase from an fp32 tile [16 columns][64 pixels] in LDS.
+//
+// A workgroup walks down a segment of TAIL_SEG = 62 output pixels (one output
+// row per item): its four waves cover the segment's 64 padded input columns,
+// halo included. The A fragments (16 pixels x 32 channels, 16 bytes per lane)
+// come straight from HBM into a register window of TAIL_ROWS input rows: each
+// item consumes three and loads one TAIL_ROWS - 3 rows ahead. (Through an LDS
+// ring filled by global_load_lds the same conv ran at 95 us at 1080p, held
+// back by the DMA issue and LDS bank conflicts.)
+constexpr int TAIL_ROWS = 6;
+constexpr int TAIL_SEG = 62;
+
+// Four workgroups per CU for C <= 64 (two for C = 96, whose row window needs
+// more than 128 VGPRs): at 1080p 64 -> 4 + DepthToSpace, 81 us with two, 70 us
+// with four.
+template <int KC, bool F32>
+__global__ void __launch_bounds__(256)
+    __attribute__((amdgpu_waves_per_eu(KC == 3 ? 2 : 4, KC == 3 ? 2 : 4)))
+conv3x3_tail(NarrowArgs a) {
+  constexpr int C = 32 * KC;
+  constexpr int PXB = 2 * C;     // bytes per pixel
+  constexpr int NR = TAIL_ROWS;  // row slots
+  constexpr int SEG = TAIL_SEG;
+  constexpr int TW = 64;         // tile row: the segment's 64 input columns
+  constexpr int TILE = 16 * TW;  // floats per tile buffer
+  extern __shared__ __attribute__((aligned(16))) float nlds[];
+  float* const tile = nlds;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+
+  const int G = gridDim.x;
+  const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int begin = (int)((int64_t)a.n_items * slot / G);
+  const int end = (int)((int64_t)a.n_items * (slot + 1) / G);
+  if (begin >= end) return;  // uniform across the workgroup
+
+  h8 wb[3][KC];
+  {
+    const h8* wp = reinterpret_cast<const h8*>(a.w) + lane;
+#pragma unroll
+    for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) wb[dy][kc] = wp[(dy * KC + kc) * 64];
+  }
+  const int m = lane & 15, kq = lane >> 4;
+  // D tile write: column lane & 15, pixels 16*wave + 4*kq .. +3.
+  const int twr = (lane & 15) * TW + 16 * wave + 4 * kq;
+
+  // Store phase: element E = ((c*b + r)*SEG*b + xq) of the item -> conv output
+  // channel k, pixel x; tile index of D[x][(0,k)], the bias, image offset.
+  const int b = a.dts_b;
+  const int64_t Wo = (int64_t)a.W * b;
+  const int64_t Ho = (int64_t)a.H * b;
+  constexpr int ELEM = F32 ? 4 : 2;
+  const int dxs = a.M * TW + 1;  // tile step from D[x][(dx,k)] to D[x+1][(dx+1,k)]
+  int s_tile[4], s_x[4];
+  float s_bias[4];
+  uint32_t s_off[4];
+  bool s_live[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * tid + i;
+    s_live[i] = e < a.M * SEG;
+    const int seg = SEG * b;
+    const int cr = e / seg;
+    const int xq = e - cr * seg;
+    const int c = cr / b, r = cr - (cr / b) * b;
+    const int x = xq / b, q = xq - (xq / b) * b;
+    const int k = (r * b + q) * a.cout + c;
+    s_tile[i] = s_live[i] ? k * TW + x : 0;
+    s_bias[i] = s_live[i] ? a.bias[k] : 0.0f;
+    s_x[i] = x;
+    s_off[i] = s_live[i] ? (uint32_t)(((int64_t)c * Ho + r) * Wo + xq) * ELEM : 0u;
+  }
+  constexpr uint32_t kOob = 0x80000000u;
+
+  int n = 0, sg = 0, h0 = 0;
+  auto decode = [&](int item) {
+    const uint32_t t = fdiv((uint32_t)item, a.fd_H);
+    h0 = item - (int)(t * (uint32_t)a.H);
+    const uint32_t nn = fdiv(t, a.fd_seg);
+    sg = (int)(t - nn * (uint32_t)a.n_seg);
+    n = (int)nn;
+  };
+  // A fragment loads through a buffer resource over image n; the lane's pixel
+  // is clamped to the last padded column (such pixels feed no stored output).
+  __amdgpu_buffer_rsrc_t irs;
+  uint32_t aoff = 0;
+  const uint32_t prow = (uint32_t)(a.Wp * PXB);
+  auto setup_run = [&]() {
+    const char* base = reinterpret_cast<const char*>(a.in) + (int64_t)n * a.Hp * a.Wp * PXB;
+    irs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(a.Hp * prow), 0x00020000);
+    int x = SEG * sg + 16 * wave + m;
+    if (x > a.Wp - 1) x = a.Wp - 1;
+    aoff = (uint32_t)(x * PXB + 16 * kq);
+  };
+  struct Row {
+    h8 v[KC];
+  };
+  auto load_row = [&](Row& R, int j) {
+    int pr = h0 + j;
+    if (pr > a.Hp - 1) pr = a.Hp - 1;
+    const uint32_t o = (uint32_t)pr * prow + aoff;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      R.v[kc] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(irs, o + 64 * kc, 0, 0));
+  };
+  int pn = 0, ps = 0, ph = 0;
+  auto store_item = [&](int tb, bool live) {
+    char* ob = reinterpret_cast<char*>(a.out) + (int64_t)pn * a.img_bytes;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, (int)a.img_bytes, 0x00020000);
+    const uint32_t item_off = (uint32_t)(((int64_t)ph * b * Wo + (int64_t)SEG * ps * b) * ELEM);
+    const float* tp = tile + tb * TILE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = (tp[s_tile[i]] + tp[s_tile[i] + dxs]) + tp[s_tile[i] + 2 * dxs];
+      v = apply_act(v + s_bias[i], a.act);
+      if (a.do_clip) v = apply_clip(v, a.clip_lo, a.clip_hi);
+      const bool ok = live && s_live[i] && (SEG * ps + s_x[i] < a.W);
+      const uint32_t off = ok ? item_off + s_off[i] : kOob;
+      if (F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, off, 0, 0);
+      } else {
+        const _Float16 hv = (_Float16)v;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, hv), rs, off, 0, 0);
+      }
+    }
+  };
+
+  // Item k of a run uses window rows k, k+1, k+2 (slots k % NR, ...), then
+  // loads row k + NR into the slot of row k; one barrier per item (the tile
+  // is double-buffered).
+  int par = 0;  // tile buffer of the current item
+  bool have_prev = false;
+  auto item = [&](Row& r0, const Row& r1, const Row& r2, int k) {
+    store_item(par ^ 1, have_prev);
+    f4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r0.v[kc], wb[0][kc], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r1.v[kc], wb[1][kc], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2.v[kc], wb[2][kc], acc, 0, 0, 0);
+    }
+    load_row(r0, k + NR);
+    *reinterpret_cast<f4*>(tile + par * TILE + twr) = acc;
+    pn = n;
+    ps = sg;
+    ph = h0 + k;
+    have_prev = true;
+    par ^= 1;
+    lds_sync();
+  };
+
+  Row W[NR];
+  for (int it = begin; it < end;) {
+    decode(it);
+    const int len = min(end - it, a.H - h0);
+    setup_run();
+#pragma unroll
+    for (int j = 0; j < NR; ++j) load_row(W[j], j);
+    // Whole cycles of the slots, then the remainder as nested conditions (one
+    // loop exit keeps the compiler's count of outstanding loads exact).
+    int k = 0;
+    for (; k + NR <= len; k += NR) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) item(W[j], W[(j + 1) % NR], W[(j + 2) % NR], k + j);
+    }
+    auto rest = [&](auto self, auto j_tag) {
+      constexpr int J = decltype(j_tag)::value;
+      if constexpr (J < NR) {
+        if (k + J < len) {
+          item(W[J], W[(J + 1) % NR], W[(J + 2) % NR], k + J);
+          self(self, IntC<J + 1>{});
+        }
+      }
+    };
+    rest(rest, IntC<0>{});
+    it += len;
+  }
+  store_item(par ^ 1, have_prev);
+}
+
 // ---------------------------------------------------------------------------
 // Direct 3x3 conv with one input channel (head conv)
 // ---------------------------------------------------------------------------
@@ -1901,13 +2091,17 @@ bool narrow_launch_eligible(const WinoArgs& w) {
   if (w.M % (b * b) != 0) return false;
   const int64_t elem = w.epi.out_kind == kOutNchwF32 ? 4 : 2;
   const int64_t img = (int64_t)w.M * w.H * w.W * elem;  // Cout * (H b) * (W b)
-  return img < ((int64_t)1 << 31);
+  const int64_t in_img = padded_rows(w.H) * padded_cols(w.W) * w.C * 2;
+  return img < ((int64_t)1 << 31) && in_img < ((int64_t)1 << 31);
 }
 
 template <int KC>
 hipError_t launch_narrow_kc(const NarrowArgs& a, bool f32, hipStream_t s) {
-  NarrowKernel fn = f32 ? conv3x3_narrow<KC, true> : conv3x3_narrow<KC, false>;
-  const size_t lds = NarrowRing<KC>::lds_bytes();
+  const bool rows = narrow_row_packed(a.M);
+  NarrowKernel fn = rows ? (f32 ? conv3x3_tail<KC, true> : conv3x3_tail<KC, false>)
+                         : (f32 ? conv3x3_narrow<KC, true> : conv3x3_narrow<KC, false>);
+  // conv3x3_tail keeps only its D tiles ([16][64] floats, two buffers) in LDS.
+  const size_t lds = rows ? (size_t)2 * 16 * 64 * 4 : NarrowRing<KC>::lds_bytes();
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1941,7 +2135,7 @@ hipError_t launch_narrow(const WinoArgs& w, hipStream_t s) {
   a.clip_hi = w.epi.clip_hi;
   a.dts_b = w.epi.dts_b >= 2 ? w.epi.dts_b : 1;
   a.cout = w.M / (a.dts_b * a.dts_b);
-  a.n_seg = (w.W + 63) / 64;
+  a.n_seg = narrow_row_packed(w.M) ? (w.W + TAIL_SEG - 1) / TAIL_SEG : (w.W + 63) / 64;
   const int64_t items = (int64_t)w.N * a.n_seg * w.H;
   if (items >= (int64_t)1 << 31) return hipErrorInvalidValue;
   a.n_items = (int32_t)items;

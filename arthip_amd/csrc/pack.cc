@@ -8,8 +8,11 @@ namespace arthip {
 
 bool narrow_eligible(int C, int M) { return C % 32 == 0 && C <= 96 && M >= 1 && M <= 16; }
 
+bool narrow_row_packed(int M) { return M >= 1 && 3 * M <= 16; }
+
 size_t narrow_packed_halfs(int C, int M) {
-  return narrow_eligible(C, M) ? static_cast<size_t>(9) * (C / 32) * 64 * 8 : 0;
+  if (!narrow_eligible(C, M)) return 0;
+  return static_cast<size_t>(narrow_row_packed(M) ? 3 : 9) * (C / 32) * 64 * 8;
 }
 
 size_t winograd_u_halfs(int C, int M) {
@@ -28,11 +31,14 @@ void winograd_pack(const float* w, int M, int C, uint16_t* out) {
   if (narrow_eligible(C, M)) {
     uint16_t* nb = out + winograd_u_halfs(C, M);
     const int kcn = C / 32;
+    const bool rows = narrow_row_packed(M);
     for (int n = 0; n < M; ++n)
       for (int c = 0; c < C; ++c)
         for (int t = 0; t < 9; ++t) {
           const int kc = c / 32, q = (c % 32) / 8, e = c % 8;
-          const size_t idx = ((static_cast<size_t>(t) * kcn + kc) * 64 + n + 16 * q) * 8 + e;
+          const int slot = rows ? t / 3 : t;             // B operand index
+          const int col = rows ? (t % 3) * M + n : n;    // B column
+          const size_t idx = ((static_cast<size_t>(slot) * kcn + kc) * 64 + col + 16 * q) * 8 + e;
           nb[idx] = f32_to_f16(w[(static_cast<size_t>(n) * C + c) * 9 + t]);
         }
   }

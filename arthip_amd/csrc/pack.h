@@ -22,10 +22,16 @@ WinoGeom winograd_geom(int C, int M);
 int direct_g8(int M);
 
 // Convs with C % 32 == 0 (C <= 96) and M <= 16 can also run as a direct conv
-// on MFMA (conv3x3_narrow, used for boundary outputs such as the model's tail).
+// on MFMA (conv3x3_tail / conv3x3_narrow, used for boundary outputs such as the
+// model's tail).
 bool narrow_eligible(int C, int M);
-// Halfs of the narrow-kernel taps: [9 taps][kc][64 lanes][8], lane = n + 16*q
-// holding w[n][32*kc + 8*q + e][tap] (v_mfma_f32_16x16x32_f16 B-operand order).
+// M <= 5: the three taps of a kernel row share one MFMA (conv3x3_tail).
+bool narrow_row_packed(int M);
+// Halfs of the direct-conv taps, in v_mfma_f32_16x16x32_f16 B-operand order
+// (lane = col + 16*q holds channels 32*kc + 8*q + e, e < 8):
+//   row-packed: [3 rows dy][kc][64 lanes][8], col = dx*M + n holding
+//               w[n][32*kc + 8*q + e][dy][dx] (zero for col >= 3M);
+//   otherwise:  [9 taps][kc][64 lanes][8], col = n holding w[n][...][tap].
 size_t narrow_packed_halfs(int C, int M);
 
 // Halfs in the packed buffer: U' as [n_ob][16 positions][kc][64 lanes][8],

@@ -108,16 +108,20 @@ def test_bench_refuses_several_gpus():
 
 def test_narrow_pack_layout():
     """C % 32 == 0 and M <= 16: the packed buffer continues after U' with the
-    direct-conv taps [tap][kc][lane][e] = w[n][32*kc + 8*(lane // 16) + e][tap],
-    n = lane % 16 (v_mfma_f32_16x16x32_f16 B-operand order), zero for n >= M."""
+    direct-conv taps in v_mfma_f32_16x16x32_f16 B-operand order (lane = col +
+    16*q holds channels 32*kc + 8*q + e). M <= 5 packs the three taps of a kernel
+    row into one operand, [dy][kc][lane][e] with col = dx*M + n; larger M keeps
+    one operand per tap, [tap][kc][lane][e] with col = n. Unused columns are zero."""
     lib = _lib.lib()
     rng = np.random.default_rng(7)
-    for c_in, m_out in [(64, 4), (32, 4), (96, 16), (64, 9)]:
+    for c_in, m_out in [(64, 4), (32, 4), (96, 5), (64, 1), (96, 16), (64, 9), (32, 6)]:
         w = (rng.standard_normal((m_out, c_in, 3, 3)) * 0.2).astype(np.float16)
         n_u = lib.arthip_conv3x3_packed_halfs(m_out, c_in)
         kc = c_in // 32
+        rows = 3 * m_out <= 16
+        n_op = 3 if rows else 9
         u_part = ((m_out + 15) // 16) * 16 * kc * 64 * 8
-        assert n_u == u_part + 9 * kc * 64 * 8
+        assert n_u == u_part + n_op * kc * 64 * 8
         n_b = lib.arthip_conv3x3_bias_len(m_out)
         u = np.zeros(n_u, np.uint16)
         b = np.zeros(n_b, np.float32)
@@ -126,13 +130,17 @@ def test_narrow_pack_layout():
             u.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n_u,
             b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n_b)
         assert rc == 0
-        nb = u[u_part:].view(np.float16).reshape(9, kc, 64, 8)
-        want = np.zeros((9, kc, 64, 8), np.float16)
+        nb = u[u_part:].view(np.float16).reshape(n_op, kc, 64, 8)
+        want = np.zeros((n_op, kc, 64, 8), np.float16)
         for lane in range(64):
-            n, q = lane % 16, lane // 16
-            if n >= m_out:
-                continue
+            col, q = lane % 16, lane // 16
             for k in range(kc):
                 for e in range(8):
-                    want[:, k, lane, e] = w[n, 32 * k + 8 * q + e].reshape(9)
+                    ch = 32 * k + 8 * q + e
+                    if rows:
+                        dx, n = divmod(col, m_out)
+                        if dx < 3:
+                            want[:, k, lane, e] = w[n, ch, :, dx]
+                    elif col < m_out:
+                        want[:, k, lane, e] = w[col, ch].reshape(9)
         np.testing.assert_array_equal(nb, want)

@@ -205,3 +205,36 @@ def test_tiny_frames(builder, hw):
     assert got.shape == want.shape
     assert np.isfinite(got).all()
     assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
+
+
+@pytest.mark.parametrize("filters,out_ch,scale,clip,io32", [
+    (64, 1, 2, None, False),      # R8F64's tail: M = 4, DepthToSpace(2)
+    (32, 1, 2, (0.0, 1.0), False),
+    (96, 1, 2, None, True),
+    (64, 5, 1, None, False),      # M = 5, plain NCHW output
+    (64, 1, 1, None, True),       # M = 1
+    (96, 3, 2, (0.0, 1.0), False),  # M = 12: one MFMA operand per tap
+    (32, 1, 3, None, False),      # M = 9
+    (64, 1, 4, None, True),       # M = 16
+])
+def test_boundary_tail_convs(filters, out_ch, scale, clip, io32):
+    """Head conv 1 -> F, then the boundary conv F -> out_ch * scale^2 with the
+    fused DepthToSpace, Clip and fp32 output: the row-packed tail kernel for
+    M <= 5 and the per-tap kernel above, on frames whose width is not a multiple
+    of the 64-pixel segment."""
+    spec = models.artcnn(0, filters, out_ch=out_ch, scale=scale, clip=clip, io_fp32=io32,
+                         global_skip=False, bias="uniform", seed=3, name="tail")
+    for h, w in [(37, 70), (9, 200)]:
+        x = models.synthetic_input((1, 1, h, w), seed=5)
+        if io32:
+            x = x.astype(np.float32)
+        with Engine(0) as e:
+            got = e.build(spec).run(x).astype(np.float32)
+        want = run_model(spec.model, x)
+        floor = run_model(spec.model, x, round_fp16=False)
+        s, f = _compare(got, want), _compare(floor, want)
+        print(filters, out_ch, scale, (h, w), s, "floor", f)
+        assert got.shape == want.shape == (1, out_ch, h * scale, w * scale)
+        assert np.isfinite(got).all()
+        assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
+        assert s["max_abs"] <= 2e-2, s
