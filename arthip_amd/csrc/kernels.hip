@@ -840,18 +840,18 @@ winograd_strip(StripArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Producer/consumer strip conv (C = M = 64, no residual inputs)
+// Producer/consumer strip conv (C = M in {64, 96}, no residual inputs)
 // ---------------------------------------------------------------------------
 //
 // The items (1 tile row x 16 tiles), fold and output staging of
 // winograd_strip, split over two kinds of waves of one 512-thread workgroup
 // per CU:
-//   * waves 0-3 (consumers) keep U' of 16 output channels each in VGPRs, run
-//     the MFMA fold and the activation into staging, and move the staged
-//     outputs of the item before to HBM;
-//   * waves 4-7 (producers) load input rows and write V'. Holding no U', they
-//     keep PIPE_ROWS - 1 row pairs in flight ahead of the transform, so HBM
-//     latency hides behind that many items of work.
+//   * waves 0 .. 2*KC-1 (consumers) keep U' of 16 output channels each in
+//     VGPRs, run the MFMA fold and the activation into staging, and move the
+//     staged outputs of the item before to HBM;
+//   * the other waves (producers) load input rows and write V'. Holding no U',
+//     they keep PipeL<KC>::NW - 1 row pairs in flight ahead of the transform,
+//     so HBM latency hides behind that many items of work.
 // Step j (one barrier each): the producers transform item j; the consumers
 // store item j-2 and fold item j-1. V' and staging are double-buffered by item
 // parity, so each buffer's writes and reads are a barrier apart. A run (the
@@ -862,40 +862,64 @@ winograd_strip(StripArgs a) {
 // 256 VGPRs the compiler keeps only one or two B reads ahead of the MFMAs.
 // Splitting the fold by position rows over 8 consumer waves (12 waves, half of
 // U' each, partial sums exchanged through LDS) ran at 137 us.
-constexpr int PIPE_ROWS = 6;
-
-// V' of an item: [position][tile][64 channels], 128-byte tile rows with the
-// channel groups of tile t at g ^ (t & 7) (as StripLds<2>); staging
-// [row][pixel][64 channels] as StripStage<2>.
-struct PipeLds {
-  static constexpr int TILES = 16;
-  static constexpr int PXS = 32;             // pixels per staged row
-  static constexpr int WPS = TILES * 64;     // halfs per position
-  static constexpr int VBUF = 16 * WPS;      // halfs per V' buffer
-  static constexpr int SBUF = 2 * PXS * 64;  // halfs per staging buffer
+//
+// C = 96: six consumer waves (192 VGPRs of U' each) and two producer waves,
+// each transforming three (tile, 4-channel) tasks per item.
+template <int KC>
+struct PipeL;
+template <>
+struct PipeL<2> {
+  static constexpr int TS = 64;  // halfs per tile row of V' (swizzled groups)
+  static constexpr int NW = 6;   // producer row-pair slots
   __host__ __device__ static constexpr int at(int t, int c) { return StripLds<2>::at(t, c); }
   __host__ __device__ static constexpr int st(int row, int x, int g) {
     return StripStage<2>::at(row, x, g);
   }
+};
+template <>
+struct PipeL<3> {
+  // 208-byte tile rows: the 16 lanes of a B read (16 tiles, one 16-byte
+  // group) land on 16 distinct bank quads. Staging rotates the 12 groups of
+  // pixel x by x >> 1.
+  static constexpr int TS = 104;
+  static constexpr int NW = 3;
+  __host__ __device__ static constexpr int at(int t, int c) { return t * TS + c; }
+  __host__ __device__ static constexpr int st(int row, int x, int g) {
+    return (row * 32 + x) * 96 + (((g + (x >> 1)) % 12) << 3);
+  }
+};
+
+template <int KC>
+struct PipeLds {
+  static constexpr int C = 32 * KC;
+  static constexpr int TILES = 16;
+  static constexpr int PXS = 32;            // pixels per staged row
+  static constexpr int WPS = TILES * PipeL<KC>::TS;  // halfs per position
+  static constexpr int VBUF = 16 * WPS;     // halfs per V' buffer
+  static constexpr int SBUF = 2 * PXS * C;  // halfs per staging buffer
+  static constexpr int NCW = 2 * KC;        // consumer waves
+  static constexpr int NPT = 64 * (8 - NCW);  // producer threads
+  static constexpr int UP = 16 * 8 * KC / NPT;  // producer tasks per thread
   static constexpr size_t lds_bytes() { return (size_t)2 * (VBUF + SBUF) * 2; }
 };
-static_assert(PipeLds::WPS == StripLds<2>::WPS && PipeLds::SBUF == StripStage<2>::SBUF,
-              "pipe and strip layouts agree");
 
-template <int ACT>
+template <int KC, int ACT>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 winograd_pipe(StripArgs a) {
-  constexpr int KC = 2;
-  constexpr int C = 32 * KC;
-  constexpr int NCW = 2 * KC;  // consumer waves
-  constexpr int NW = PIPE_ROWS;
-  using L = PipeLds;
+  using L = PipeLds<KC>;
+  using LL = PipeL<KC>;
+  constexpr int C = L::C;
+  constexpr int NCW = L::NCW;
+  constexpr int NW = LL::NW;
+  constexpr int UP = L::UP;
   constexpr int WPS = L::WPS;
   constexpr int VBUF = L::VBUF;
   constexpr int SBUF = L::SBUF;
   constexpr int PXS = L::PXS;
+  constexpr int GR = C / 8;  // 16-byte groups per pixel
   constexpr int QUADS = C / 4;
   constexpr int PX = 2 * C;
+  static_assert(L::NPT * UP == 16 * QUADS, "producer tasks cover the item");
   extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];  // 2 V' + 2 staging buffers
   _Float16* const stg = vlds + 2 * VBUF;
   const int tid = threadIdx.x;
@@ -935,12 +959,13 @@ winograd_pipe(StripArgs a) {
     const f4 bias4 = *reinterpret_cast<const f4*>(a.bias + ch0);
     const _Float16* vr0[KC];
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) vr0[kc] = vlds + L::at(tcol, 32 * kc + 8 * kq);
-    const int sw0 = L::st(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
+    for (int kc = 0; kc < KC; ++kc) vr0[kc] = vlds + LL::at(tcol, 32 * kc + 8 * kq);
+    // Pixels 2*tcol and 2*tcol + 1 share the staging rotation.
+    const int sw0 = LL::st(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
     // Store mapping: thread handles 16-byte group sg of pixel sx in both rows.
-    const int sx = tid >> 3;
-    const int sg = tid & 7;
-    const int sr0 = L::st(0, sx, sg);
+    const int sx = tid / GR;
+    const int sg = tid - sx * GR;
+    const int sr0 = LL::st(0, sx, sg);
     const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
     const uint32_t rb32 = (uint32_t)row_bytes;
     const int n_rec = (int)(rb32 + PXS * PX);
@@ -1037,42 +1062,54 @@ winograd_pipe(StripArgs a) {
   }
 
   // ---- producers: step j transforms item j ---------------------------------
+  // Task v of thread p: flat index p + NPT * v -> tile, 4-channel quad.
   const int ptid = tid - 64 * NCW;
-  const int tt = ptid / QUADS;
-  const int tq = ptid - tt * QUADS;
-  _Float16* const vw0 = vlds + L::at(tt, 4 * tq);
-  uint32_t in_lane = 0;
+  int tt[UP];
+  uint32_t tq4[UP];
+  _Float16* vw0[UP];
+#pragma unroll
+  for (int v = 0; v < UP; ++v) {
+    const int f = ptid + L::NPT * v;
+    tt[v] = f / QUADS;
+    tq4[v] = (uint32_t)(4 * (f - tt[v] * QUADS));
+    vw0[v] = vlds + LL::at(tt[v], (int)tq4[v]);
+  }
+  uint32_t in_lane[UP];
   auto in_row = [&](int r) {
     if (r > a.Hp - 2) r = a.Hp - 2;
     return reinterpret_cast<const char*>(a.in) + (((int64_t)n * a.Hp + r) * a.Wp + PXS * s) * PX;
   };
-  auto load2 = [&](h2 (&x)[16], const char* rb) {
+  auto load2 = [&](h2 (&x)[UP][16], const char* rb) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int v = 0; v < UP; ++v)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const h4 v = *reinterpret_cast<const h4*>(rb + r * row_bytes + in_lane + j * PX);
-        x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
-        x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
-      }
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const h4 q = *reinterpret_cast<const h4*>(rb + r * row_bytes + in_lane[v] + j * PX);
+          x[v][2 * (4 * r + j)] = __builtin_shufflevector(q, q, 0, 1);
+          x[v][2 * (4 * r + j) + 1] = __builtin_shufflevector(q, q, 2, 3);
+        }
   };
   int par = 0;  // parity of step j = parity of item j
-  auto step = [&](h2 (&top)[16], h2 (&bot)[16]) {
-    v_transform<WPS>(vw0 + par * VBUF, top, bot);
+  auto step = [&](h2 (&top)[UP][16], h2 (&bot)[UP][16]) {
+#pragma unroll
+    for (int v = 0; v < UP; ++v) v_transform<WPS>(vw0[v] + par * VBUF, top[v], bot[v]);
     load2(top, in_row(2 * (th + NW)));
     ++th;
     par ^= 1;
     lds_sync();
   };
 
-  h2 W[NW][16];
+  h2 W[NW][UP][16];
   for (int it = begin; it < end;) {
     decode(it);
     const int len = min(end - it, a.tiles_h - th);
-    {
+#pragma unroll
+    for (int v = 0; v < UP; ++v) {
       // Tiles past the right edge read tile 0's patch (never stored).
-      const int t = (L::TILES * s + tt < a.tiles_w) ? tt : 0;
-      in_lane = (uint32_t)(2 * t * C + 4 * tq) * 2;
+      const int t = (L::TILES * s + tt[v] < a.tiles_w) ? tt[v] : 0;
+      in_lane[v] = (uint32_t)(2 * t * C + (int)tq4[v]) * 2;
     }
 #pragma unroll
     for (int m = 0; m < NW; ++m) load2(W[m], in_row(2 * (th + m)));
@@ -2008,11 +2045,31 @@ StripKernel strip_kernel_act(int act, int nskip) {
   }
 }
 
-// winograd_strip covers C == M in {32, 64} with the fast epilogue.
+// winograd_strip covers C == M in {32, 64} with the fast epilogue;
+// winograd_pipe covers C == M in {64, 96} without residual inputs.
 bool strip_eligible(const WinoArgs& a) {
-  return a.C == a.M && (a.C == 32 || a.C == 64) && a.epi.out_kind == kOutPadded &&
-         a.epi.dts_b < 2 && !a.epi.do_clip &&
-         (a.epi.act == kActNone || a.epi.act == kActRelu || a.epi.act == kActSilu);
+  const bool fast_epi = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && !a.epi.do_clip &&
+                        (a.epi.act == kActNone || a.epi.act == kActRelu ||
+                         a.epi.act == kActSilu);
+  if (!fast_epi || a.C != a.M) return false;
+  if (a.C == 32 || a.C == 64) return true;
+  return a.C == 96 && a.epi.skip0 == nullptr && a.epi.skip1 == nullptr;
+}
+
+template <int KC>
+hipError_t launch_pipe(const StripArgs& a, int act, hipStream_t s) {
+  StripKernel pf = act == kActRelu   ? winograd_pipe<KC, kActRelu>
+                   : act == kActSilu ? winograd_pipe<KC, kActSilu>
+                                     : winograd_pipe<KC, kActNone>;
+  const size_t lds = PipeLds<KC>::lds_bytes();
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  int64_t grid = cu_count();  // one 512-thread workgroup per CU
+  if (grid > a.n_items) grid = a.n_items;
+  grid = (grid + 7) / 8 * 8;
+  hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(512), lds, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
@@ -2038,20 +2095,9 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
   a.fd_tiles_h = make_fastdiv((uint32_t)a.tiles_h);
   a.fd_strips = make_fastdiv((uint32_t)a.n_strips);
   const int kc = w.C / 32;
-  if (kc == 2 && nskip == 0) {
-    StripKernel pf = w.epi.act == kActRelu   ? winograd_pipe<kActRelu>
-                     : w.epi.act == kActSilu ? winograd_pipe<kActSilu>
-                                             : winograd_pipe<kActNone>;
-    const size_t lds = PipeLds::lds_bytes();
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    int64_t grid = cu_count();
-    if (grid > items) grid = items;
-    grid = (grid + 7) / 8 * 8;
-    hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(512), lds, s, a);
-    return hipGetLastError();
-  }
+  if (nskip == 0 && kc == 2) return launch_pipe<2>(a, w.epi.act, s);
+  if (nskip == 0 && kc == 3) return launch_pipe<3>(a, w.epi.act, s);
+  if (kc > 2) return hipErrorInvalidValue;
   StripKernel fn = kc == 1 ? strip_kernel_act<1>(w.epi.act, nskip)
                            : strip_kernel_act<2>(w.epi.act, nskip);
   if (fn == nullptr) return hipErrorInvalidValue;

@@ -233,3 +233,37 @@ def test_strip_tiny(h, w):
 def test_head_tiny(h, w):
     x, wt, b = make_case(22, 2, 1, 64, h, w)
     check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), f"head {h}x{w}")
+
+
+# C == M in {64, 96} without residual inputs runs the producer/consumer kernel
+# (winograd_pipe): the same strips, with the producers' row window restarting
+# at every strip boundary of a workgroup's item range.
+@pytest.mark.parametrize("c", [64, 96])
+@pytest.mark.parametrize("h,w", GEOMETRY)
+def test_pipe_geometry(c, h, w):
+    x, wt, b = make_case(30, 1, c, c, h, w)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), f"pipe{c} {h}x{w}")
+
+
+@pytest.mark.parametrize("c", [64, 96])
+@pytest.mark.parametrize("h,w", TINY)
+def test_pipe_tiny(c, h, w):
+    x, wt, b = make_case(31, 1, c, c, h, w)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), f"pipe{c} {h}x{w}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_pipe_epilogue_c96(act):
+    x, wt, b = make_case(32, 1, 96, 96, 21, 70)
+    check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"pipe96 act{act}")
+
+
+def test_pipe_batch_odd_c96():
+    x, wt, b = make_case(33, 3, 96, 96, 17, 45)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), "pipe96 batch3 17x45")
+
+
+def test_pipe_long_runs_c96():
+    # 135 tile rows x 10 strips over 256 workgroups: ranges cross strips.
+    x, wt, b = make_case(34, 1, 96, 96, 270, 320)
+    check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), "pipe96 270x320")
