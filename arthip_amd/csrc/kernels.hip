@@ -840,7 +840,7 @@ winograd_strip(StripArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Producer/consumer strip conv (C = M in {64, 96}, no residual inputs)
+// Producer/consumer strip conv (C = M in {64, 96})
 // ---------------------------------------------------------------------------
 //
 // The items (1 tile row x 16 tiles), fold and output staging of
@@ -856,6 +856,12 @@ winograd_strip(StripArgs a) {
 // store item j-2 and fold item j-1. V' and staging are double-buffered by item
 // parity, so each buffer's writes and reads are a barrier apart. A run (the
 // items of one strip) restarts the producers' row window.
+//
+// Residual inputs: the producers load item j's residual tile in step j (ahead
+// of their row prefetch, so that waiting for it leaves the prefetch in flight)
+// and write it in step j+1 to a double-buffered LDS tile in the staging layout
+// (two inputs are added there in fp16, s0 + s1); the consumers add it to the
+// staged output when they store the item in step j+2.
 //
 // Measured on the 1080p 64 -> 64 ReLU conv: 145 us with winograd_strip, 122 us
 // here. Items of 32 tiles (two MFMA column blocks per wave) ran at 146 us: at
@@ -900,10 +906,13 @@ struct PipeLds {
   static constexpr int NCW = 2 * KC;        // consumer waves
   static constexpr int NPT = 64 * (8 - NCW);  // producer threads
   static constexpr int UP = 16 * 8 * KC / NPT;  // producer tasks per thread
-  static constexpr size_t lds_bytes() { return (size_t)2 * (VBUF + SBUF) * 2; }
+  static constexpr int SKC = 2 * PXS * (C / 8) / NPT;  // residual chunks per producer thread
+  static constexpr size_t lds_bytes(int nskip) {
+    return (size_t)2 * (VBUF + SBUF + (nskip > 0 ? SBUF : 0)) * 2;
+  }
 };
 
-template <int KC, int ACT>
+template <int KC, int ACT, int NSKIP>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 winograd_pipe(StripArgs a) {
   using L = PipeLds<KC>;
@@ -920,8 +929,10 @@ winograd_pipe(StripArgs a) {
   constexpr int QUADS = C / 4;
   constexpr int PX = 2 * C;
   static_assert(L::NPT * UP == 16 * QUADS, "producer tasks cover the item");
-  extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];  // 2 V' + 2 staging buffers
+  // 2 V' | 2 staging | 2 residual tiles (with residual inputs)
+  extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
   _Float16* const stg = vlds + 2 * VBUF;
+  _Float16* const skt = stg + 2 * SBUF;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -934,6 +945,9 @@ winograd_pipe(StripArgs a) {
   const int K = end - begin;
 
   const int64_t row_bytes = (int64_t)a.Wp * PX;
+  const uint32_t rb32 = (uint32_t)row_bytes;
+  const int n_rec = (int)(rb32 + L::PXS * PX);  // bytes of an item's two output rows
+  constexpr uint32_t kOob = 0x80000000u;
   int n, s, th;
   auto decode = [&](int item) {
     const uint32_t sgl = fdiv((uint32_t)item, a.fd_tiles_h);
@@ -967,11 +981,8 @@ winograd_pipe(StripArgs a) {
     const int sg = tid - sx * GR;
     const int sr0 = LL::st(0, sx, sg);
     const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
-    const uint32_t rb32 = (uint32_t)row_bytes;
-    const int n_rec = (int)(rb32 + PXS * PX);
-    constexpr uint32_t kOob = 0x80000000u;
 
-    // Item `item` from staging buffer SB; absent items and pixels past the
+    // Item `item` from staging buffer SB (plus its residual tile); absent items and pixels past the
     // edges get out-of-range offsets, so every step issues the same two stores.
     auto store_item = [&](int item, bool live, int SB) {
       decode(item);
@@ -981,7 +992,8 @@ winograd_pipe(StripArgs a) {
           __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, n_rec, 0x00020000);
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * PXS * C);
+        h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * PXS * C);
+        if (NSKIP > 0) v += *reinterpret_cast<const h8*>(skt + SB * SBUF + sr0 + r * PXS * C);
         const bool ok = live && (PXS * s + sx < a.W) && (r == 0 || 2 * th + 1 < a.H);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs,
                                                ok ? (uint32_t)r * rb32 + s_lane : kOob, 0,
@@ -1092,9 +1104,60 @@ winograd_pipe(StripArgs a) {
         }
   };
   int par = 0;  // parity of step j = parity of item j
+
+  // Residual tile chunks of this thread: chunk f = ptid + NPT * i -> row,
+  // pixel, 16-byte group; LDS offset in the staging layout, lane byte offset
+  // within the item's two output rows.
+  constexpr int SKC = L::SKC;
+  int sk_lds[NSKIP > 0 ? SKC : 1];
+  uint32_t sk_off[NSKIP > 0 ? SKC : 1];
+  int sk_x[NSKIP > 0 ? SKC : 1], sk_r[NSKIP > 0 ? SKC : 1];
+  h8 skv[NSKIP > 0 ? NSKIP : 1][NSKIP > 0 ? SKC : 1];
+  if (NSKIP > 0) {
+#pragma unroll
+    for (int i = 0; i < SKC; ++i) {
+      const int f = ptid + L::NPT * i;
+      const int r = f / (PXS * GR);
+      const int x = (f / GR) % PXS;
+      const int g = f % GR;
+      sk_lds[i] = LL::st(r, x, g);
+      sk_off[i] = (uint32_t)r * rb32 + (uint32_t)(x * C + g * 8) * 2;
+      sk_x[i] = x;
+      sk_r[i] = r;
+    }
+  }
+  // Loads item (n, s, th)'s residual tile into skv (out-of-range offsets read
+  // zero past the edges).
+  auto load_skips = [&]() {
+    const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + PXS * s + 1;
+#pragma unroll
+    for (int k = 0; k < NSKIP; ++k) {
+      const char* sb = reinterpret_cast<const char*>(k == 0 ? a.skip0 : a.skip1) + pix0 * PX;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)sb, (short)0, n_rec, 0x00020000);
+#pragma unroll
+      for (int i = 0; i < SKC; ++i) {
+        const bool ok = (PXS * s + sk_x[i] < a.W) && (sk_r[i] == 0 || 2 * th + 1 < a.H);
+        skv[k][i] = __builtin_bit_cast(
+            h8, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? sk_off[i] : kOob, 0, kNonTemporal));
+      }
+    }
+  };
+  // Writes the residual tile loaded in the step before to buffer SB.
+  auto write_skips = [&](int SB) {
+#pragma unroll
+    for (int i = 0; i < SKC; ++i) {
+      h8 v = skv[0][i];
+      if (NSKIP > 1) v += skv[1][i];
+      *reinterpret_cast<h8*>(skt + SB * SBUF + sk_lds[i]) = v;
+    }
+  };
+
   auto step = [&](h2 (&top)[UP][16], h2 (&bot)[UP][16]) {
+    if (NSKIP > 0) write_skips(par ^ 1);  // item j-1 (garbage for j == 0, never stored)
 #pragma unroll
     for (int v = 0; v < UP; ++v) v_transform<WPS>(vw0[v] + par * VBUF, top[v], bot[v]);
+    if (NSKIP > 0) load_skips();
     load2(top, in_row(2 * (th + NW)));
     ++th;
     par ^= 1;
@@ -1134,7 +1197,8 @@ winograd_pipe(StripArgs a) {
     rest(rest, IntC<0>{});
     it += len;
   }
-  lds_sync();  // step K
+  if (NSKIP > 0) write_skips(par ^ 1);  // step K: item K-1
+  lds_sync();
   lds_sync();  // step K + 1
 }
 
@@ -2046,22 +2110,21 @@ StripKernel strip_kernel_act(int act, int nskip) {
 }
 
 // winograd_strip covers C == M in {32, 64} with the fast epilogue;
-// winograd_pipe covers C == M in {64, 96} without residual inputs.
+// winograd_pipe covers C == M = 64 without residual inputs and C == M = 96.
 bool strip_eligible(const WinoArgs& a) {
   const bool fast_epi = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && !a.epi.do_clip &&
                         (a.epi.act == kActNone || a.epi.act == kActRelu ||
                          a.epi.act == kActSilu);
   if (!fast_epi || a.C != a.M) return false;
-  if (a.C == 32 || a.C == 64) return true;
-  return a.C == 96 && a.epi.skip0 == nullptr && a.epi.skip1 == nullptr;
+  return a.C == 32 || a.C == 64 || a.C == 96;
 }
 
-template <int KC>
+template <int KC, int NSKIP>
 hipError_t launch_pipe(const StripArgs& a, int act, hipStream_t s) {
-  StripKernel pf = act == kActRelu   ? winograd_pipe<KC, kActRelu>
-                   : act == kActSilu ? winograd_pipe<KC, kActSilu>
-                                     : winograd_pipe<KC, kActNone>;
-  const size_t lds = PipeLds<KC>::lds_bytes();
+  StripKernel pf = act == kActRelu   ? winograd_pipe<KC, kActRelu, NSKIP>
+                   : act == kActSilu ? winograd_pipe<KC, kActSilu, NSKIP>
+                                     : winograd_pipe<KC, kActNone, NSKIP>;
+  const size_t lds = PipeLds<KC>::lds_bytes(NSKIP);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
@@ -2095,9 +2158,16 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
   a.fd_tiles_h = make_fastdiv((uint32_t)a.tiles_h);
   a.fd_strips = make_fastdiv((uint32_t)a.n_strips);
   const int kc = w.C / 32;
-  if (nskip == 0 && kc == 2) return launch_pipe<2>(a, w.epi.act, s);
-  if (nskip == 0 && kc == 3) return launch_pipe<3>(a, w.epi.act, s);
-  if (kc > 2) return hipErrorInvalidValue;
+  // 64 channels with residual inputs stay on winograd_strip (it runs at the
+  // streaming rate there).
+  if (nskip == 0 && kc == 2) return launch_pipe<2, 0>(a, w.epi.act, s);
+  if (kc == 3) {
+    switch (nskip) {
+      case 0: return launch_pipe<3, 0>(a, w.epi.act, s);
+      case 1: return launch_pipe<3, 1>(a, w.epi.act, s);
+      default: return launch_pipe<3, 2>(a, w.epi.act, s);
+    }
+  }
   StripKernel fn = kc == 1 ? strip_kernel_act<1>(w.epi.act, nskip)
                            : strip_kernel_act<2>(w.epi.act, nskip);
   if (fn == nullptr) return hipErrorInvalidValue;

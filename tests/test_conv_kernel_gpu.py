@@ -267,3 +267,24 @@ def test_pipe_long_runs_c96():
     # 135 tile rows x 10 strips over 256 workgroups: ranges cross strips.
     x, wt, b = make_case(34, 1, 96, 96, 270, 320)
     check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), "pipe96 270x320")
+
+
+@pytest.mark.parametrize("nskip", [1, 2])
+@pytest.mark.parametrize("h,w", [(8, 17), (17, 33), (33, 17), (1082, 64), (54, 1920)])
+def test_pipe_residual_c96(nskip, h, w):
+    """96 channels with residual inputs: the producers stage the residual tile
+    in LDS a step ahead (two inputs pre-added in fp16)."""
+    x, wt, b = make_case(35, 1, 96, 96, h, w)
+    rng = np.random.default_rng(36)
+    skips = [rng.standard_normal((1, 96, h, w)).astype(np.float16) for _ in range(nskip)]
+    check(run_conv(x, wt, b, 1, skips), oracle_conv(x, wt, b, 1, skips),
+          f"pipe96 skip{nskip} {h}x{w}")
+
+
+def test_pipe_residual_c96_batch_tiny():
+    for n, h, w in [(3, 17, 45), (1, 1, 1), (2, 3, 5), (1, 2, 33)]:
+        x, wt, b = make_case(37, n, 96, 96, h, w)
+        rng = np.random.default_rng(38)
+        skips = [rng.standard_normal((n, 96, h, w)).astype(np.float16) for _ in range(2)]
+        check(run_conv(x, wt, b, 2, skips), oracle_conv(x, wt, b, 2, skips),
+              f"pipe96 skip2 {n}x{h}x{w}")
