@@ -1734,28 +1734,24 @@ __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
   }
 }
 
-// Row-segment variant for the fast epilogue (padded NHWC output, M % 8 == 0):
-// a work item is one output row x SEG pixels, SEG = 4 * 256 / G8. The three
-// input rows of the next item are loaded into registers while the current
-// item computes and then stored to the other of two LDS buffers (one barrier
-// per item). Thread t computes pixels 4q .. 4q+3 (q = t / G8) for channels
-// 8g .. 8g+7 (g = t % G8) from a 3 x 6 window read from LDS, and stores the four
-// 16-byte pixel vectors through a buffer resource spanning the segment's valid
-// pixels (stores past the right edge are dropped by its range check). The
-// stores take the nontemporal policy: measured at 1080p the head conv goes from
-// 81 to 75 us and the next conv, which reads this output, from 157 to 145 us.
-template <int G8>
-struct HeadSeg {
-  static constexpr int SEG = 4 * 256 / G8;
-  static constexpr int ROW = SEG + 4;           // LDS halfs per input row (SEG + 2 used)
-  static constexpr int NV = (3 * (SEG + 2) + 255) / 256;  // input values per thread
-};
+// Column-walking variant for the fast epilogue (padded NHWC output, M % 8 ==
+// 0): a work item is one output row x SEG pixels, SEG = 4 * 256 / G8, and a
+// workgroup's item range walks down a column of segments. Thread t computes
+// pixels 4q .. 4q+3 (q = t / G8) for channels 8g .. 8g+7 (g = t % G8). Its 3 x 6
+// input window comes straight from HBM: a register ring of HEAD_ROWS padded
+// input rows (six halfs each, three 4-byte buffer loads), one row loaded per
+// item HEAD_ROWS - 3 rows ahead, so there is no LDS and no barrier. Columns
+// past a row's end read the next row (or zero past the image) and feed only
+// pixels beyond the right edge, whose stores the output buffer resource drops.
+// (With the window staged through LDS per item, 8 items per workgroup: 75-81 us
+// at 1080p 1 -> 64.)
+constexpr int HEAD_ROWS = 6;
 
-template <int G8>
-__global__ void __launch_bounds__(256) direct_conv_c1_rows(DirectArgs a, int n_seg, int n_items,
+template <int G8, int ACT, bool SKIP>
+__global__ void __launch_bounds__(256) direct_conv_c1_walk(DirectArgs a, int n_seg, int n_items,
                                                            FastDiv fd_seg, FastDiv fd_H) {
-  using S = HeadSeg<G8>;
-  __shared__ __attribute__((aligned(16))) _Float16 rows[2][3 * S::ROW];
+  constexpr int SEG = 4 * 256 / G8;
+  constexpr int NR = HEAD_ROWS;
   const int tid = threadIdx.x;
   const int g = tid % G8;
   const int q = tid / G8;
@@ -1774,65 +1770,55 @@ __global__ void __launch_bounds__(256) direct_conv_c1_rows(DirectArgs a, int n_s
     b0 = *reinterpret_cast<const f4*>(a.epi.bias + ch0);
     b1 = *reinterpret_cast<const f4*>(a.epi.bias + ch0 + 4);
   }
-  const _Float16* in = reinterpret_cast<const _Float16*>(a.in);
 
   const int G = gridDim.x;
   const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
   const int begin = (int)((int64_t)n_items * slot / G);
   const int end = (int)((int64_t)n_items * (slot + 1) / G);
-  if (begin >= end) return;  // uniform across the workgroup
+  if (begin >= end) return;
 
-  auto coords = [&](int item, int& n, int& h, int& x0) {
-    const uint32_t t = fdiv((uint32_t)item, fd_seg);
-    x0 = (item - (int)(t * (uint32_t)n_seg)) * S::SEG;
-    const uint32_t nn = fdiv(t, fd_H);
-    h = (int)(t - nn * (uint32_t)a.H);
+  // Item = (n * n_seg + segment) * H + output row.
+  int n = 0, sgm = 0, h0 = 0;
+  auto decode = [&](int item) {
+    const uint32_t t = fdiv((uint32_t)item, fd_H);
+    h0 = item - (int)(t * (uint32_t)a.H);
+    const uint32_t nn = fdiv(t, fd_seg);
+    sgm = (int)(t - nn * (uint32_t)n_seg);
     n = (int)nn;
   };
-  // Input values of an item: element e = r * (SEG + 2) + x of padded rows
-  // h .. h+2, padded columns x0 .. x0 + SEG + 1 (clamped to the row).
-  _Float16 v[S::NV];
-  auto load_item = [&](int item) {
-    int n, h, x0;
-    coords(item, n, h, x0);
-#pragma unroll
-    for (int i = 0; i < S::NV; ++i) {
-      const int e = tid + 256 * i;
-      const int r = e / (S::SEG + 2);
-      int x = x0 + e - r * (S::SEG + 2);
-      if (x > a.Wp - 1) x = a.Wp - 1;
-      v[i] = e < 3 * (S::SEG + 2) ? in[((int64_t)n * a.Hp + h + r) * a.Wp + x] : (_Float16)0.0f;
-    }
+  __amdgpu_buffer_rsrc_t irs;
+  uint32_t col_off = 0;
+  const uint32_t prow = (uint32_t)a.Wp * 2;
+  auto setup_run = [&]() {
+    const char* base = reinterpret_cast<const char*>(a.in) + (int64_t)n * a.Hp * a.Wp * 2;
+    irs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(a.Hp * prow), 0x00020000);
+    col_off = (uint32_t)(sgm * SEG + 4 * q) * 2;
   };
-  auto store_item = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < S::NV; ++i) {
-      const int e = tid + 256 * i;
-      const int r = e / (S::SEG + 2);
-      if (e < 3 * (S::SEG + 2)) rows[buf][r * S::ROW + e - r * (S::SEG + 2)] = v[i];
-    }
+  struct Row {
+    h2 v[3];  // padded columns x .. x+5 of one input row
   };
-
-  load_item(begin);
-  store_item(0);
-  if (begin + 1 < end) load_item(begin + 1);
-  __syncthreads();
-  for (int it = begin, buf = 0; it < end; ++it, buf ^= 1) {
-    int n, h, x0;
-    coords(it, n, h, x0);
-    // 3 x 6 window of pixels 4q .. 4q+3.
+  auto load_row = [&](Row& R, int pr) {
+    if (pr > a.Hp - 1) pr = a.Hp - 1;
+    const uint32_t o = (uint32_t)pr * prow + col_off;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      R.v[i] = __builtin_bit_cast(h2, __builtin_amdgcn_raw_buffer_load_b32(irs, o + 4 * i, 0, 0));
+  };
+  auto item = [&](Row& r0, const Row& r1, const Row& r2, int k) {
+    const int h = h0 + k;
     _Float16 x[3][6];
+    const Row* rr[3] = {&r0, &r1, &r2};
 #pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      const _Float16* rp = &rows[buf][r * S::ROW + 4 * q];
-      const h4 lo = *reinterpret_cast<const h4*>(rp);
-      const h2 hi = *reinterpret_cast<const h2*>(rp + 4);
-      x[r][0] = lo[0]; x[r][1] = lo[1]; x[r][2] = lo[2]; x[r][3] = lo[3];
-      x[r][4] = hi[0]; x[r][5] = hi[1];
-    }
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        x[r][2 * i] = rr[r]->v[i][0];
+        x[r][2 * i + 1] = rr[r]->v[i][1];
+      }
+    const int x0 = sgm * SEG;
     char* ob = reinterpret_cast<char*>(a.epi.out) +
                (((int64_t)n * a.Hp + h + 1) * a.Wp + x0 + 1) * a.M * 2;
-    const int valid = min(S::SEG, a.W - x0);
+    const int valid = min(SEG, a.W - x0);
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, valid * a.M * 2, 0x00020000);
 #pragma unroll
@@ -1845,48 +1831,64 @@ __global__ void __launch_bounds__(256) direct_conv_c1_rows(DirectArgs a, int n_s
       for (int c = 0; c < 4; ++c) {
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-          s0 = __builtin_amdgcn_fdot2(xv[k], wr[c][k], s0, false);
-          s1 = __builtin_amdgcn_fdot2(xv[k], wr[c + 4][k], s1, false);
+        for (int kk = 0; kk < 5; ++kk) {
+          s0 = __builtin_amdgcn_fdot2(xv[kk], wr[c][kk], s0, false);
+          s1 = __builtin_amdgcn_fdot2(xv[kk], wr[c + 4][kk], s1, false);
         }
         acc0[c] = s0;
         acc1[c] = s1;
       }
       const uint32_t off = (uint32_t)((4 * q + j) * a.M + ch0) * 2;
       h4 s00 = {0, 0, 0, 0}, s01 = s00, s10 = s00, s11 = s00;
-      const int64_t pix = ((int64_t)n * a.Hp + h + 1) * a.Wp + x0 + 1 + 4 * q + j;
-      if (live && x0 + 4 * q + j < a.W) {
-        if (a.epi.skip0) {
-          const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip0) + pix * a.M + ch0;
-          s00 = *reinterpret_cast<const h4*>(sp);
-          s01 = *reinterpret_cast<const h4*>(sp + 4);
-        }
-        if (a.epi.skip1) {
-          const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip1) + pix * a.M + ch0;
-          s10 = *reinterpret_cast<const h4*>(sp);
-          s11 = *reinterpret_cast<const h4*>(sp + 4);
+      if (SKIP) {
+        const int64_t pix = ((int64_t)n * a.Hp + h + 1) * a.Wp + x0 + 1 + 4 * q + j;
+        if (live && x0 + 4 * q + j < a.W) {
+          if (a.epi.skip0) {
+            const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip0) + pix * a.M + ch0;
+            s00 = *reinterpret_cast<const h4*>(sp);
+            s01 = *reinterpret_cast<const h4*>(sp + 4);
+          }
+          if (a.epi.skip1) {
+            const _Float16* sp = reinterpret_cast<const _Float16*>(a.epi.skip1) + pix * a.M + ch0;
+            s10 = *reinterpret_cast<const h4*>(sp);
+            s11 = *reinterpret_cast<const h4*>(sp + 4);
+          }
         }
       }
-      h4 r0, r1;
-      if (a.epi.act == kActRelu) {
-        r0 = fast4<kActRelu>(acc0, b0, s00, s10);
-        r1 = fast4<kActRelu>(acc1, b1, s01, s11);
-      } else if (a.epi.act == kActSilu) {
-        r0 = fast4<kActSilu>(acc0, b0, s00, s10);
-        r1 = fast4<kActSilu>(acc1, b1, s01, s11);
-      } else {
-        r0 = fast4<kActNone>(acc0, b0, s00, s10);
-        r1 = fast4<kActNone>(acc1, b1, s01, s11);
-      }
-      const h8 rv = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+      const h4 v0 = fast4<ACT>(acc0, b0, s00, s10);
+      const h4 v1 = fast4<ACT>(acc1, b1, s01, s11);
+      const h8 rv = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, rv), rs,
                                              live ? off : 0x80000000u, 0, kNonTemporal);
     }
-    if (it + 1 < end) {
-      store_item(buf ^ 1);
-      if (it + 2 < end) load_item(it + 2);
+    load_row(r0, h + NR);
+  };
+
+  Row W[NR];
+  for (int it = begin; it < end;) {
+    decode(it);
+    const int len = min(end - it, a.H - h0);
+    setup_run();
+#pragma unroll
+    for (int j = 0; j < NR; ++j) load_row(W[j], h0 + j);
+    // Whole cycles of the slots, then the remainder as nested conditions (one
+    // loop exit keeps the compiler's count of outstanding loads exact).
+    int k = 0;
+    for (; k + NR <= len; k += NR) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) item(W[j], W[(j + 1) % NR], W[(j + 2) % NR], k + j);
     }
-    __syncthreads();
+    auto rest = [&](auto self, auto j_tag) {
+      constexpr int J = decltype(j_tag)::value;
+      if constexpr (J < NR) {
+        if (k + J < len) {
+          item(W[J], W[(J + 1) % NR], W[(J + 2) % NR], k + J);
+          self(self, IntC<J + 1>{});
+        }
+      }
+    };
+    rest(rest, IntC<0>{});
+    it += len;
   }
 }
 
@@ -2332,20 +2334,32 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
   if (fast && a.g8 <= 16) {
     const int seg = 4 * 256 / a.g8;
     const int n_seg = (a.W + seg - 1) / seg;
-    const int64_t items = (int64_t)a.N * a.H * n_seg;
+    const int64_t items = (int64_t)a.N * n_seg * a.H;
     if (items < ((int64_t)1 << 31)) {
       const FastDiv fs = make_fastdiv((uint32_t)n_seg), fh = make_fastdiv((uint32_t)a.H);
-      int64_t grid = (int64_t)cu_count() * 8;  // 8 workgroups per CU (vs 4: 81 -> 76 us)
+      using HeadKernel = void (*)(DirectArgs, int, int, FastDiv, FastDiv);
+      const bool sk = a.epi.skip0 != nullptr || a.epi.skip1 != nullptr;
+      const int act = a.epi.act == kActRelu ? 1 : (a.epi.act == kActSilu ? 2 : 0);
+      auto pick = [&](auto g_tag) -> HeadKernel {
+        constexpr int GG = decltype(g_tag)::value;
+        static const HeadKernel t[2][3] = {
+            {direct_conv_c1_walk<GG, kActNone, false>, direct_conv_c1_walk<GG, kActRelu, false>,
+             direct_conv_c1_walk<GG, kActSilu, false>},
+            {direct_conv_c1_walk<GG, kActNone, true>, direct_conv_c1_walk<GG, kActRelu, true>,
+             direct_conv_c1_walk<GG, kActSilu, true>}};
+        return t[sk][act];
+      };
+      HeadKernel fn = a.g8 == 1 ? pick(IntC<1>{}) : a.g8 == 2 ? pick(IntC<2>{})
+                    : a.g8 == 4 ? pick(IntC<4>{}) : a.g8 == 8 ? pick(IntC<8>{}) : pick(IntC<16>{});
+      int occ = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), 256,
+                                                       0) != hipSuccess ||
+          occ < 1)
+        occ = 1;
+      int64_t grid = (int64_t)cu_count() * occ;  // every workgroup resident
       if (grid > items) grid = items;
       grid = (grid + 7) / 8 * 8;
-      const dim3 gd((unsigned)grid), bd(256);
-      switch (a.g8) {
-        case 1: hipLaunchKernelGGL(direct_conv_c1_rows<1>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
-        case 2: hipLaunchKernelGGL(direct_conv_c1_rows<2>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
-        case 4: hipLaunchKernelGGL(direct_conv_c1_rows<4>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
-        case 8: hipLaunchKernelGGL(direct_conv_c1_rows<8>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
-        default: hipLaunchKernelGGL(direct_conv_c1_rows<16>, gd, bd, 0, s, a, n_seg, (int)items, fs, fh); break;
-      }
+      hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, s, a, n_seg, (int)items, fs, fh);
       return hipGetLastError();
     }
   }
