@@ -103,7 +103,10 @@ struct NarrowArgs {
 
 // Direct 3x3 conv for a single input channel (the model's head conv).
 struct DirectArgs {
-  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][1]
+  // in_kind 0: padded NHWC fp16 [N][Hp][Wp][1]; 1 / 2: the engine's NCHW
+  // boundary input [N][1][H][W] in fp16 / fp32 (head conv reading it directly).
+  const void* in;
+  int32_t in_kind;
   const uint16_t* w;   // packed taps: [g8][8 ch][5 x half2] (direct_pack)
   Epilogue epi;
   int32_t N, H, W, M;

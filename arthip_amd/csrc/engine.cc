@@ -296,10 +296,33 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
     return false;
   };
 
-  // Boundary input -> internal padded tensor.
+  // Boundary input -> internal padded tensor, unless its only reader is a
+  // one-channel head conv on the fast path (padded output, M % 8 == 0, no
+  // Clip or residual input): that conv reads the NCHW boundary input itself.
   const Shape sin = shapes.at(graph_.input_name);
-  if (!alloc(graph_.input_name, sin, -1)) return fail();
-  {
+  int fused_in_op = -1;
+  if (sin.c == 1 && graph_.output_name != graph_.input_name) {
+    int readers = 0, reader = -1;
+    bool other_use = false;
+    for (int i = 0; i < nops; ++i) {
+      if (ops[i].in0 == graph_.input_name) {
+        ++readers;
+        reader = i;
+      }
+      other_use = other_use || ops[i].in1 == graph_.input_name;
+      for (const auto& s : ops[i].skips) other_use = other_use || s == graph_.input_name;
+    }
+    if (readers == 1 && !other_use && ops[reader].kind == OpKind::Conv) {
+      const Op& op = ops[reader];
+      const int64_t m = graph_.weights.at(op.weight).dims[0];
+      const bool to_boundary = direct_out && reader == final_op;
+      if (!to_boundary && m % 8 == 0 && m <= 128 && !op.clip && op.dts_b < 1 && op.skips.empty() &&
+          sin.n * sin.h * ((sin.w + 1023) / 4) < ((int64_t)1 << 31))
+        fused_in_op = reader;
+    }
+  }
+  if (fused_in_op < 0) {
+    if (!alloc(graph_.input_name, sin, -1)) return fail();
     Step st;
     st.kind = StepKind::InputConvert;
     st.in = kBoundaryIn;
@@ -321,7 +344,12 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
 
     Step st;
     st.op = i;
-    st.in = tbuf.at(op.in0);
+    if (i == fused_in_op) {
+      st.in = kBoundaryIn;
+      st.in_kind = graph_.input_fp32 ? 2 : 1;
+    } else {
+      st.in = tbuf.at(op.in0);
+    }
     st.out = out_buf;
     st.N = (int32_t)si.n; st.H = (int32_t)si.h; st.W = (int32_t)si.w; st.C = (int32_t)si.c;
     switch (op.kind) {
@@ -446,7 +474,8 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
         epi.out = ptr(st.out);
         if (st.kind == StepKind::ConvDirect) {
           DirectArgs a{};
-          a.in = static_cast<const uint16_t*>(ptr(st.in));
+          a.in = ptr(st.in);
+          a.in_kind = st.in_kind;
           a.w = static_cast<const uint16_t*>(wbufs_[st.wbuf].ptr);
           a.epi = epi;
           a.N = st.N; a.H = st.H; a.W = st.W; a.M = st.M;

@@ -49,6 +49,7 @@ struct Step {
   int32_t dts_b = 0, out_kind = kOutPadded, do_clip = 0;
   float lo = 0.0f, hi = 0.0f;
   int32_t fp32 = 0;  // IO steps: boundary side is fp32
+  int32_t in_kind = 0;  // direct conv reading the boundary input: 1 fp16, 2 fp32
 };
 
 class Engine {

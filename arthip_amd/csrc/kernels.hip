@@ -586,7 +586,6 @@ template <int KC, int ACT, int NSKIP>
 __global__ void __launch_bounds__(128 * KC) __attribute__((amdgpu_waves_per_eu(2, 2)))
 winograd_strip(StripArgs a) {
   constexpr int C = 32 * KC;   // input channels = output channels
-  constexpr int NT = 128 * KC; // threads
   constexpr int WPS = StripLds<KC>::WPS;
   constexpr int VBUF = StripLds<KC>::VBUF;
   constexpr int SBUF = StripStage<KC>::SBUF;
@@ -1744,10 +1743,12 @@ __global__ void __launch_bounds__(256) direct_conv_c1(DirectArgs a) {
 // past a row's end read the next row (or zero past the image) and feed only
 // pixels beyond the right edge, whose stores the output buffer resource drops.
 // (With the window staged through LDS per item, 8 items per workgroup: 75-81 us
-// at 1080p 1 -> 64.)
+// at 1080p 1 -> 64.) BIN 1 / 2: the input is the engine's NCHW boundary tensor
+// (fp16 / fp32, converted with round-to-nearest-even) instead of the padded
+// copy; the window is then read element by element, zero outside the image.
 constexpr int HEAD_ROWS = 6;
 
-template <int G8, int ACT, bool SKIP>
+template <int G8, int ACT, bool SKIP, int BIN>
 __global__ void __launch_bounds__(256) direct_conv_c1_walk(DirectArgs a, int n_seg, int n_items,
                                                            FastDiv fd_seg, FastDiv fd_H) {
   constexpr int SEG = 4 * 256 / G8;
@@ -1788,21 +1789,43 @@ __global__ void __launch_bounds__(256) direct_conv_c1_walk(DirectArgs a, int n_s
   };
   __amdgpu_buffer_rsrc_t irs;
   uint32_t col_off = 0;
-  const uint32_t prow = (uint32_t)a.Wp * 2;
+  constexpr int EB = BIN == 2 ? 4 : 2;  // bytes per input element
+  const uint32_t prow = (uint32_t)(BIN ? a.W : a.Wp) * EB;
   auto setup_run = [&]() {
-    const char* base = reinterpret_cast<const char*>(a.in) + (int64_t)n * a.Hp * a.Wp * 2;
-    irs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(a.Hp * prow), 0x00020000);
-    col_off = (uint32_t)(sgm * SEG + 4 * q) * 2;
+    const int64_t img = BIN ? (int64_t)a.H * a.W : (int64_t)a.Hp * a.Wp;
+    const char* base = reinterpret_cast<const char*>(a.in) + (int64_t)n * img * EB;
+    irs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(img * EB), 0x00020000);
+    col_off = (uint32_t)(sgm * SEG + 4 * q) * EB;
   };
   struct Row {
     h2 v[3];  // padded columns x .. x+5 of one input row
   };
   auto load_row = [&](Row& R, int pr) {
     if (pr > a.Hp - 1) pr = a.Hp - 1;
-    const uint32_t o = (uint32_t)pr * prow + col_off;
+    if (BIN == 0) {
+      const uint32_t o = (uint32_t)pr * prow + col_off;
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-      R.v[i] = __builtin_bit_cast(h2, __builtin_amdgcn_raw_buffer_load_b32(irs, o + 4 * i, 0, 0));
+      for (int i = 0; i < 3; ++i)
+        R.v[i] = __builtin_bit_cast(h2, __builtin_amdgcn_raw_buffer_load_b32(irs, o + 4 * i, 0, 0));
+    } else {
+      // Padded column x + i is image column x + i - 1 of image row pr - 1.
+      const int hr = pr - 1;
+      const int c0 = sgm * SEG + 4 * q - 1;
+      const bool row_ok = hr >= 0 && hr < a.H;
+      _Float16 e[6];
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        const int c = c0 + i;
+        const uint32_t o =
+            row_ok && c >= 0 && c < a.W ? ((uint32_t)hr * (uint32_t)a.W + (uint32_t)c) * EB : 0x80000000u;
+        if (BIN == 1)
+          e[i] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(irs, o, 0, 0));
+        else
+          e[i] = (_Float16)__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(irs, o, 0, 0));
+      }
+#pragma unroll
+      for (int i = 0; i < 3; ++i) R.v[i] = h2{e[2 * i], e[2 * i + 1]};
+    }
   };
   auto item = [&](Row& r0, const Row& r1, const Row& r2, int k) {
     const int h = h0 + k;
@@ -2318,6 +2341,8 @@ int direct_g8(int M) {
 }
 
 hipError_t launch_direct(DirectArgs a, hipStream_t s) {
+  // Only the column-walking fast path reads the NCHW boundary input; the
+  // engine plans that fusion exactly when the fast path applies.
   a.g8 = direct_g8(a.M);
   a.Hp = (int32_t)padded_rows(a.H);
   a.Wp = (int32_t)padded_cols(a.W);
@@ -2339,15 +2364,23 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
       const FastDiv fs = make_fastdiv((uint32_t)n_seg), fh = make_fastdiv((uint32_t)a.H);
       using HeadKernel = void (*)(DirectArgs, int, int, FastDiv, FastDiv);
       const bool sk = a.epi.skip0 != nullptr || a.epi.skip1 != nullptr;
+      if (a.in_kind != 0 && sk) return hipErrorInvalidValue;
       const int act = a.epi.act == kActRelu ? 1 : (a.epi.act == kActSilu ? 2 : 0);
+      // Rows: padded input without / with residual inputs, then the NCHW
+      // boundary input in fp16 and fp32 (never with residual inputs).
+      const int variant = a.in_kind == 0 ? (sk ? 1 : 0) : 1 + a.in_kind;
       auto pick = [&](auto g_tag) -> HeadKernel {
         constexpr int GG = decltype(g_tag)::value;
-        static const HeadKernel t[2][3] = {
-            {direct_conv_c1_walk<GG, kActNone, false>, direct_conv_c1_walk<GG, kActRelu, false>,
-             direct_conv_c1_walk<GG, kActSilu, false>},
-            {direct_conv_c1_walk<GG, kActNone, true>, direct_conv_c1_walk<GG, kActRelu, true>,
-             direct_conv_c1_walk<GG, kActSilu, true>}};
-        return t[sk][act];
+        static const HeadKernel t[4][3] = {
+            {direct_conv_c1_walk<GG, kActNone, false, 0>, direct_conv_c1_walk<GG, kActRelu, false, 0>,
+             direct_conv_c1_walk<GG, kActSilu, false, 0>},
+            {direct_conv_c1_walk<GG, kActNone, true, 0>, direct_conv_c1_walk<GG, kActRelu, true, 0>,
+             direct_conv_c1_walk<GG, kActSilu, true, 0>},
+            {direct_conv_c1_walk<GG, kActNone, false, 1>, direct_conv_c1_walk<GG, kActRelu, false, 1>,
+             direct_conv_c1_walk<GG, kActSilu, false, 1>},
+            {direct_conv_c1_walk<GG, kActNone, false, 2>, direct_conv_c1_walk<GG, kActRelu, false, 2>,
+             direct_conv_c1_walk<GG, kActSilu, false, 2>}};
+        return t[variant][act];
       };
       HeadKernel fn = a.g8 == 1 ? pick(IntC<1>{}) : a.g8 == 2 ? pick(IntC<2>{})
                     : a.g8 == 4 ? pick(IntC<4>{}) : a.g8 == 8 ? pick(IntC<8>{}) : pick(IntC<16>{});
@@ -2363,6 +2396,7 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
       return hipGetLastError();
     }
   }
+  if (a.in_kind != 0) return hipErrorInvalidValue;
   if (fast)
     hipLaunchKernelGGL(direct_conv_c1<true>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
   else
