@@ -238,3 +238,46 @@ def test_boundary_tail_convs(filters, out_ch, scale, clip, io32):
         assert np.isfinite(got).all()
         assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
         assert s["max_abs"] <= 2e-2, s
+
+
+def _steps(engine, x):
+    engine.set_profiling(True)
+    engine.profile_read()
+    got = engine.run(x)
+    names = [n for n, _, _ in engine.profile_read()]
+    engine.set_profiling(False)
+    return got, names
+
+
+@pytest.mark.parametrize("io32", [False, True])
+def test_head_reads_boundary_input(io32):
+    """A one-channel input read only by the head conv goes straight into the
+    head kernel (no input conversion step); an input that is also a residual
+    operand keeps its padded copy. Both match the oracle."""
+    spec = models.artcnn(1, 32, io_fp32=io32, bias="uniform", seed=7, name="head_in")
+    x = models.synthetic_input((1, 1, 23, 70), seed=8)
+    if io32:
+        x = x.astype(np.float32)
+    with Engine(0) as e:
+        got, names = _steps(e.build(spec), x)
+    assert not any(n.startswith("input_convert") for n in names), names
+    want = run_model(spec.model, x)
+    floor = run_model(spec.model, x, round_fp16=False)
+    s, f = _compare(got.astype(np.float32), want), _compare(floor, want)
+    assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
+
+    # Same model with the graph input added to the tail's output: the input
+    # is now also a residual operand.
+    b = models._Builder(7, "uniform", io32)
+    xin = "xh" if io32 else "x"
+    h = b.conv(xin, 1, 8, "relu")
+    t = b.conv(h, 8, 1)
+    y = b.add(t, xin, "res")
+    m = b.finish(xin, y, 1, 1)
+    with Engine(0) as e:
+        got2, names2 = _steps(e.build(m), x)
+    assert any(n.startswith("input_convert") for n in names2), names2
+    want2 = run_model(m, x)
+    floor2 = run_model(m, x, round_fp16=False)
+    s2, f2 = _compare(got2.astype(np.float32), want2), _compare(floor2, want2)
+    assert s2["rel_rms"] <= max(4 * f2["rel_rms"], 2e-3), (s2, f2)
