@@ -21,6 +21,34 @@ class LibraryMissing(RuntimeError):
     """libarthip.so has not been built (run arthip_amd.build.build())."""
 
 
+class VsFormat(ctypes.Structure):
+    """arthip_vs_format (VSVideoFormat's fields the filter reads)."""
+    _fields_ = [("color_family", ctypes.c_int), ("sample_type", ctypes.c_int),
+                ("bits_per_sample", ctypes.c_int), ("sub_sampling_w", ctypes.c_int),
+                ("sub_sampling_h", ctypes.c_int), ("num_planes", ctypes.c_int)]
+
+
+class VsModelArgs(ctypes.Structure):
+    """arthip_vs_model_args (hip.Model's arguments)."""
+    _fields_ = [("network_path", ctypes.c_char_p), ("network_data", ctypes.c_void_p),
+                ("network_size", ctypes.c_size_t),
+                ("has_device_id", ctypes.c_int), ("device_id", ctypes.c_int64),
+                ("has_num_streams", ctypes.c_int), ("num_streams", ctypes.c_int64),
+                ("has_fp16", ctypes.c_int), ("fp16", ctypes.c_int64),
+                ("overlap", ctypes.POINTER(ctypes.c_int64)), ("overlap_len", ctypes.c_int),
+                ("tilesize", ctypes.POINTER(ctypes.c_int64)), ("tilesize_len", ctypes.c_int),
+                ("flexible_output_prop", ctypes.c_char_p)]
+
+
+class VsModelInfo(ctypes.Structure):
+    """arthip_vs_model_info (the output clip)."""
+    _fields_ = [("format", VsFormat), ("width", ctypes.c_int), ("height", ctypes.c_int),
+                ("num_planes", ctypes.c_int), ("planes_written", ctypes.c_int),
+                ("flexible", ctypes.c_int), ("in_fp32", ctypes.c_int), ("out_fp32", ctypes.c_int),
+                ("num_streams", ctypes.c_int), ("scale_w", ctypes.c_int),
+                ("scale_h", ctypes.c_int)]
+
+
 def _declare(lib: ctypes.CDLL) -> None:
     c_int, c_size, c_void, c_char = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_char_p
     i32p = ctypes.POINTER(ctypes.c_int)
@@ -59,6 +87,18 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("engine_alloc_failure_then_run", c_int, c_char, c_int, c_int, c_int, c_int, c_int,
         c_void, c_size, c_void, c_size, sizep, i32p, i64p, i32p, c_char, c_int, c_char, c_int)
 
+    fmtp = ctypes.POINTER(VsFormat)
+    ptrs = ctypes.POINTER(c_void)
+    pdp = ctypes.POINTER(ctypes.c_ssize_t)
+    sig("arthip_vs_model_create", c_int, ctypes.POINTER(VsModelArgs), c_int, fmtp, c_int, c_int,
+        ctypes.POINTER(c_void), ctypes.POINTER(VsModelInfo), c_char, c_int)
+    sig("arthip_vs_model_get_frame", c_int, c_void, fmtp, i32p, i32p, ptrs, pdp, ptrs, pdp, c_int,
+        c_char, c_int)
+    sig("arthip_vs_model_destroy", None, c_void)
+    sig("arthip_vs_version", c_int, c_char, c_int, i32p)
+    sig("arthip_vs_device_properties", c_int, c_int, c_char, c_int, i64p, i64p, i64p, c_char,
+        c_int)
+
     sig("arthip_conv3x3_packed_halfs", c_size, c_int, c_int)
     sig("arthip_conv3x3_bias_len", c_size, c_int)
     sig("arthip_conv3x3_pack", c_int, u16p, u16p, c_int, c_int, u16p, c_size, f32p, c_size)
@@ -68,6 +108,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_padded_dims", c_int, c_int, c_int, i32p, i32p)
     sig("arthip_f32_to_f16", ctypes.c_uint16, ctypes.c_float)
     sig("arthip_f16_to_f32", ctypes.c_float, ctypes.c_uint16)
+    sig("arthip_f32_to_f16_no_subnormals", ctypes.c_uint16, ctypes.c_float)
     sig("arthip_last_error", c_char)
     sig("arthip_version", c_char)
 
@@ -79,9 +120,11 @@ EXPORTED_SYMBOLS = (
     "arthip_engine_run", "arthip_engine_run_device", "arthip_engine_describe",
     "arthip_engine_set_profiling", "arthip_engine_profile_read",
     "engine_device_count", "engine_probe", "engine_run", "engine_alloc_failure_then_run",
+    "arthip_vs_model_create", "arthip_vs_model_get_frame", "arthip_vs_model_destroy",
+    "arthip_vs_version", "arthip_vs_device_properties",
     "arthip_conv3x3_packed_halfs", "arthip_conv3x3_bias_len", "arthip_conv3x3_pack",
     "arthip_conv3x3_f16_nhwc", "arthip_conv3x3_limits", "arthip_padded_dims", "arthip_f32_to_f16",
-    "arthip_f16_to_f32", "arthip_last_error", "arthip_version",
+    "arthip_f16_to_f32", "arthip_f32_to_f16_no_subnormals", "arthip_last_error", "arthip_version",
 )
 
 

@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "arthip.h"
+#include "clip.h"
 #include "engine.h"
 #include "half.h"
 #include "launch.h"
@@ -14,6 +15,10 @@
 
 struct arthip_engine {
   std::unique_ptr<arthip::Engine> eng;
+};
+
+struct arthip_vs_model {
+  std::unique_ptr<arthip::ClipModel> m;
 };
 
 namespace {
@@ -272,11 +277,118 @@ int engine_alloc_failure_then_run(const char* model_path, int N, int bigH, int b
 }
 
 // ---------------------------------------------------------------------------
+// VapourSynth filter core
+// ---------------------------------------------------------------------------
+
+static arthip::VideoFormat to_format(const arthip_vs_format& f) {
+  arthip::VideoFormat v;
+  v.color_family = f.color_family;
+  v.sample_type = f.sample_type;
+  v.bits_per_sample = f.bits_per_sample;
+  v.sub_sampling_w = f.sub_sampling_w;
+  v.sub_sampling_h = f.sub_sampling_h;
+  v.num_planes = f.num_planes;
+  return v;
+}
+
+int arthip_vs_model_create(const arthip_vs_model_args* args, int num_clips,
+                           const arthip_vs_format* clip_format, int width, int height,
+                           arthip_vs_model** out, arthip_vs_model_info* info, char* err,
+                           int errlen) {
+  if (out == nullptr || args == nullptr || clip_format == nullptr)
+    return report("hip.Model: null argument", ARTHIP_ERR_BUILD, err, errlen);
+  *out = nullptr;
+  arthip::ClipModelArgs a;
+  if (args->network_size > 0 && args->network_data != nullptr) {
+    const uint8_t* p = static_cast<const uint8_t*>(args->network_data);
+    a.network_bytes.assign(p, p + args->network_size);
+  } else if (args->network_path != nullptr) {
+    a.network_path = args->network_path;
+  } else {
+    return report("hip.Model: network_path is required", ARTHIP_ERR_BUILD, err, errlen);
+  }
+  a.has_device_id = args->has_device_id != 0;
+  a.device_id = args->device_id;
+  a.has_num_streams = args->has_num_streams != 0;
+  a.num_streams = args->num_streams;
+  a.has_fp16 = args->has_fp16 != 0;
+  a.fp16 = args->fp16;
+  if (args->overlap && args->overlap_len > 0)
+    a.overlap.assign(args->overlap, args->overlap + args->overlap_len);
+  if (args->tilesize && args->tilesize_len > 0)
+    a.tilesize.assign(args->tilesize, args->tilesize + args->tilesize_len);
+  if (args->flexible_output_prop) a.flexible_output_prop = args->flexible_output_prop;
+  std::string e;
+  auto m = arthip::ClipModel::Create(a, num_clips, to_format(*clip_format), width, height, e);
+  if (!m) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  if (info) {
+    const arthip::VideoFormat& f = m->out_format();
+    info->format = arthip_vs_format{f.color_family, f.sample_type, f.bits_per_sample,
+                                    f.sub_sampling_w, f.sub_sampling_h, f.num_planes};
+    info->width = m->out_width();
+    info->height = m->out_height();
+    info->num_planes = m->out_channels();
+    info->planes_written = m->planes_written();
+    info->flexible = m->flexible() ? 1 : 0;
+    info->in_fp32 = m->input_fp32() ? 1 : 0;
+    info->out_fp32 = m->output_fp32() ? 1 : 0;
+    info->num_streams = m->num_streams();
+    info->scale_w = m->scale_w();
+    info->scale_h = m->scale_h();
+  }
+  auto h = std::make_unique<arthip_vs_model>();
+  h->m = std::move(m);
+  *out = h.release();
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int arthip_vs_model_get_frame(arthip_vs_model* model, const arthip_vs_format* fmt,
+                              const int* plane_w, const int* plane_h, const void* const* src,
+                              const ptrdiff_t* src_stride, void* const* dst,
+                              const ptrdiff_t* dst_stride, int n_dst, char* err, int errlen) {
+  if (model == nullptr || fmt == nullptr)
+    return report("hip.Model: null model or format", ARTHIP_ERR_RUN, err, errlen);
+  std::string e;
+  if (!model->m->GetFrame(to_format(*fmt), plane_w, plane_h, src, src_stride, dst, dst_stride,
+                          n_dst, e))
+    return report(e, ARTHIP_ERR_RUN, err, errlen);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+void arthip_vs_model_destroy(arthip_vs_model* model) { delete model; }
+
+int arthip_vs_version(char* version, int len, int* device_count) {
+  copy_out(arthip_version(), version, len);
+  if (device_count) {
+    int n = 0;
+    *device_count = hipGetDeviceCount(&n) == hipSuccess ? n : -1;
+  }
+  return ARTHIP_OK;
+}
+
+int arthip_vs_device_properties(int device_id, char* name, int namelen, int64_t* pci_device_id,
+                                int64_t* clock_rate, int64_t* global_memory, char* err,
+                                int errlen) {
+  hipDeviceProp_t props{};
+  if (hipGetDeviceProperties(&props, device_id) != hipSuccess)
+    return report("hipDeviceProperties: failed to query device", ARTHIP_ERR_BUILD, err, errlen);
+  copy_out(props.name, name, namelen);
+  if (pci_device_id) *pci_device_id = props.pciDeviceID;
+  if (clock_rate) *clock_rate = props.clockRate;
+  if (global_memory) *global_memory = static_cast<int64_t>(props.totalGlobalMem);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Kernel-level entry points
 // ---------------------------------------------------------------------------
 
 uint16_t arthip_f32_to_f16(float f) { return arthip::f32_to_f16(f); }
 float arthip_f16_to_f32(uint16_t h) { return arthip::f16_to_f32(h); }
+uint16_t arthip_f32_to_f16_no_subnormals(float f) { return arthip::f32_to_f16_no_subnormals(f); }
 const char* arthip_last_error(void) { return t_last_error.c_str(); }
 const char* arthip_version(void) { return "arthip-mi355x 0.1.0 (gfx950)"; }
 

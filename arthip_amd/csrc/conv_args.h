@@ -144,4 +144,16 @@ struct IoArgs {
   int32_t fp32;  // boundary side is fp32
 };
 
+// Element types of VapourSynth plane samples and of the engine boundary.
+enum SampleKind : int32_t { kSampleU8 = 0, kSampleU16 = 1, kSampleF16 = 2, kSampleF32 = 3 };
+
+// Element-wise conversion between plane samples and the NCHW boundary:
+// u8 / u16 / f16 / f32 -> f16 / f32 (input side) and f16 -> u16 (output side).
+struct PlaneArgs {
+  const void* src;
+  void* dst;
+  int64_t n;  // elements
+  int32_t src_kind, dst_kind;  // SampleKind
+};
+
 }  // namespace arthip

@@ -65,24 +65,24 @@ bool Engine::Init(std::string& error) {
   return true;
 }
 
-bool Engine::Build(const void* data, size_t size, std::string& error) {
+bool Engine::Build(const void* data, size_t size, std::string& error, const BuildOptions& opts) {
   std::lock_guard<std::mutex> lock(mu_);
   onnx::Model model;
   if (!onnx::ParseModel(data, size, model, error)) return false;
   FreeAll();
   built_ = false;
-  if (!BuildGraph(model, graph_, error)) return false;
+  if (!BuildGraph(model, graph_, error, opts)) return false;
   built_ = true;
   return true;
 }
 
-bool Engine::BuildFile(const std::string& path, std::string& error) {
+bool Engine::BuildFile(const std::string& path, std::string& error, const BuildOptions& opts) {
   std::lock_guard<std::mutex> lock(mu_);
   onnx::Model model;
   if (!onnx::LoadModelFile(path, model, error)) return false;
   FreeAll();
   built_ = false;
-  if (!BuildGraph(model, graph_, error)) return false;
+  if (!BuildGraph(model, graph_, error, opts)) return false;
   built_ = true;
   return true;
 }

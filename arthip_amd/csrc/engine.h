@@ -64,8 +64,10 @@ class Engine {
   // models can be parsed and validated without a GPU.
   bool Init(std::string& error);
 
-  bool Build(const void* data, size_t size, std::string& error);
-  bool BuildFile(const std::string& path, std::string& error);
+  bool Build(const void* data, size_t size, std::string& error,
+             const BuildOptions& opts = BuildOptions());
+  bool BuildFile(const std::string& path, std::string& error,
+                 const BuildOptions& opts = BuildOptions());
 
   bool OutputShape(const int64_t in_nchw[4], int64_t out_nchw[4]) const;
   bool InputFp32() const { return graph_.input_fp32; }

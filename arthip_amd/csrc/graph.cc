@@ -102,7 +102,8 @@ bool Materialize(const onnx::Tensor& t, Weight& w, std::string& error) {
 
 }  // namespace
 
-bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error) {
+bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error,
+                const BuildOptions& opts) {
   g = Graph();
   const onnx::Graph& og = model.graph;
 
@@ -112,7 +113,20 @@ bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error) {
       error = "initializer #" + std::to_string(i) + " has no name";
       return false;
     }
-    if (!Materialize(t, g.weights[t.name], error)) return false;
+    Weight& w = g.weights[t.name];
+    if (!Materialize(t, w, error)) return false;
+    if (opts.fp16 && w.dtype == onnx::kFloat) {
+      const size_t n = w.data.size() / 4;
+      std::vector<uint8_t> h(n * 2);
+      for (size_t k = 0; k < n; ++k) {
+        float f;
+        std::memcpy(&f, w.data.data() + 4 * k, 4);
+        const uint16_t b = f32_to_f16_no_subnormals(f);
+        std::memcpy(h.data() + 2 * k, &b, 2);
+      }
+      w.data.swap(h);
+      w.dtype = onnx::kFloat16;
+    }
   }
 
   // The activation input is the first graph input that is not an initializer
@@ -140,8 +154,9 @@ bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error) {
   // Boundary Casts (fp32 graph IO around an fp16 body) fold into the IO
   // conversion; bare fp32 IO is handled the same way (hip_engine.cc:338-373).
   std::vector<bool> consumed(og.nodes.size(), false);
+  const bool keep32 = !opts.fp16 || opts.keep_io_fp32;
   if (gin->elem_type == onnx::kFloat) {
-    g.input_fp32 = true;
+    g.input_fp32 = keep32;
     for (int i = 0; i < static_cast<int>(og.nodes.size()); ++i) {
       const auto& n = og.nodes[i];
       if (n.op_type == "Cast" && !n.inputs.empty() && n.inputs[0] == g.input_name &&
@@ -153,7 +168,7 @@ bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error) {
     }
   }
   if (gout.elem_type == onnx::kFloat) {
-    g.output_fp32 = true;
+    g.output_fp32 = keep32;
     for (int i = 0; i < static_cast<int>(og.nodes.size()); ++i) {
       const auto& n = og.nodes[i];
       if (n.op_type == "Cast" && !n.outputs.empty() && n.outputs[0] == g.output_name &&

@@ -72,9 +72,21 @@ struct Shape {
 int MaxConvInputChannels();
 int MaxConvOutputChannels();
 
+// Load-time conversion of an fp32 model to fp16, as the VapourSynth filter
+// applies it with fp16=1 (src/vapoursynth/vs_hip.cpp:503-515, through
+// convert_float_to_float16 with force_fp16_initializers): fp32 initializers are
+// rounded with the converter's rule (f32_to_f16_no_subnormals), and fp32 graph
+// inputs / outputs become fp16 unless keep_io_fp32 keeps them behind boundary
+// Casts (the converter's cast_input / cast_output).
+struct BuildOptions {
+  bool fp16 = false;
+  bool keep_io_fp32 = false;
+};
+
 // Parses, validates and fuses. Error messages keep the reference's wording
 // where its tests match on them (tests/correctness/test_engine.py).
-bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error);
+bool BuildGraph(const onnx::Model& model, Graph& g, std::string& error,
+                const BuildOptions& opts = BuildOptions());
 
 // NCHW input shape -> NHWC shape of every activation. Fails on geometry the
 // kernels cannot run (channel mismatch, residual/binary shape mismatch,

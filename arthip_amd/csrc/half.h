@@ -40,6 +40,21 @@ inline uint16_t f32_to_f16(float f) {
   return static_cast<uint16_t>(sign | bits);
 }
 
+// fp32 -> fp16 as the reference's load-time model converter rounds
+// initializers (src/vapoursynth/convert_float_to_float16.cpp:165-186): round to
+// nearest even for results in the normal range, but every |x| < 2^-14 (the
+// smallest normal half) becomes a signed zero instead of a subnormal, and NaN
+// becomes a signed inf.
+inline uint16_t f32_to_f16_no_subnormals(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t a = x & 0x7fffffffu;
+  if (a >= 0x7f800000u) return static_cast<uint16_t>(sign | 0x7c00u);
+  if (a < 0x38800000u) return static_cast<uint16_t>(sign);  // |x| < 2^-14
+  return f32_to_f16(f);
+}
+
 inline float f16_to_f32(uint16_t h) {
   const uint32_t sign = (static_cast<uint32_t>(h) & 0x8000u) << 16;
   const uint32_t e = (h >> 10) & 0x1fu;

@@ -2035,6 +2035,41 @@ __global__ void __launch_bounds__(256) output_convert(IoArgs a) {
   }
 }
 
+// VapourSynth plane samples <-> NCHW boundary elements, one element per
+// thread step (src/vapoursynth/vs_hip.cpp:175-225 packs on the host,
+// 347-369 unpacks integer output):
+// - integer samples scale by 1/255 (8 bit) or 1/65535 (16 bit) with one fp32
+//   multiply, then round to fp16 (nearest even) or stay fp32;
+// - fp16 widens exactly to fp32, fp32 rounds to fp16;
+// - fp16 -> u16 (integer output) is trunc(v * 65535 + 0.5) in fp32 with no
+//   fused multiply-add, clamped to [0, 65535] (NaN -> 0); the reference's cast
+//   is undefined outside that range.
+__device__ __forceinline__ float plane_load(const void* p, int64_t i, int kind) {
+  switch (kind) {
+    case kSampleU8: return (float)reinterpret_cast<const uint8_t*>(p)[i] * (1.0f / 255.0f);
+    case kSampleU16: return (float)reinterpret_cast<const uint16_t*>(p)[i] * (1.0f / 65535.0f);
+    case kSampleF16: return (float)reinterpret_cast<const _Float16*>(p)[i];
+    default: return reinterpret_cast<const float*>(p)[i];
+  }
+}
+
+__global__ void __launch_bounds__(256) plane_convert(PlaneArgs a) {
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = plane_load(a.src, i, a.src_kind);
+    if (a.dst_kind == kSampleF16) {
+      reinterpret_cast<_Float16*>(a.dst)[i] = (_Float16)v;
+    } else if (a.dst_kind == kSampleF32) {
+      reinterpret_cast<float*>(a.dst)[i] = v;
+    } else {
+      const float x = v * 65535.0f + 0.5f;
+      const float c = x >= 65535.0f ? 65535.0f : (x > 0.0f ? x : 0.0f);
+      reinterpret_cast<uint16_t*>(a.dst)[i] = (uint16_t)(uint32_t)c;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -2426,6 +2461,16 @@ hipError_t launch_input_convert(IoArgs a, hipStream_t s) {
 hipError_t launch_output_convert(IoArgs a, hipStream_t s) {
   const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
   hipLaunchKernelGGL(output_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_plane_convert(PlaneArgs a, hipStream_t s) {
+  const bool src_ok = a.src_kind >= kSampleU8 && a.src_kind <= kSampleF32;
+  const bool dst_ok = a.dst_kind == kSampleF16 || a.dst_kind == kSampleF32 ||
+                      (a.dst_kind == kSampleU16 && a.src_kind == kSampleF16);
+  if (!src_ok || !dst_ok || a.n < 0) return hipErrorInvalidValue;
+  if (a.n == 0) return hipSuccess;
+  hipLaunchKernelGGL(plane_convert, dim3(grid_for(a.n, 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -18,5 +18,6 @@ hipError_t launch_eltwise(EltArgs a, bool binary, hipStream_t s);
 hipError_t launch_dts(DtsArgs a, hipStream_t s);
 hipError_t launch_input_convert(IoArgs a, hipStream_t s);
 hipError_t launch_output_convert(IoArgs a, hipStream_t s);
+hipError_t launch_plane_convert(PlaneArgs a, hipStream_t s);
 
 }  // namespace arthip

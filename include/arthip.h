@@ -111,6 +111,105 @@ int engine_alloc_failure_then_run(const char* model_path, int N, int bigH, int b
                                   int runerrlen);
 
 /* ------------------------------------------------------------------------ */
+/* VapourSynth filter core: hip.Model, Version and DeviceProperties          */
+/* (src/vapoursynth/vs_hip.cpp:401-591, 77-385, 597-641) with VapourSynth's   */
+/* types replaced by plain formats and plane pointers. A VapourSynth adapter  */
+/* maps the filter's VSMap arguments into arthip_vs_model_args, calls         */
+/* arthip_vs_model_create from its create callback and                        */
+/* arthip_vs_model_get_frame from getFrame (fmParallel-safe). Error texts     */
+/* carry the reference's "hip.Model: " prefix and wording.                    */
+/* ------------------------------------------------------------------------ */
+
+typedef struct arthip_vs_model arthip_vs_model;
+
+/* VSVideoFormat's fields that the filter reads. color_family uses
+ * VSColorFamily (0 undefined, 1 gray, 2 RGB, 3 YUV); sample_type uses
+ * VSSampleType (0 integer, 1 float). */
+typedef struct arthip_vs_format {
+  int color_family;
+  int sample_type;
+  int bits_per_sample;
+  int sub_sampling_w;
+  int sub_sampling_h;
+  int num_planes;
+} arthip_vs_format;
+
+/* hip.Model's arguments (vs_hip.cpp:628-637). has_* = 0 marks an absent
+ * optional; overlap / tilesize with length 0 and a NULL or empty
+ * flexible_output_prop are absent. network_data / network_size, when
+ * network_size > 0, replace network_path with serialized model bytes. */
+typedef struct arthip_vs_model_args {
+  const char* network_path;
+  const void* network_data;
+  size_t network_size;
+  int has_device_id;
+  int64_t device_id;
+  int has_num_streams;
+  int64_t num_streams;
+  int has_fp16;
+  int64_t fp16;
+  const int64_t* overlap;
+  int overlap_len;
+  const int64_t* tilesize;
+  int tilesize_len;
+  const char* flexible_output_prop;
+} arthip_vs_model_args;
+
+/* The output clip (vs_hip.cpp:554-581). num_planes is the model's final
+ * output channel count (the flexible protocol's "num_planes");
+ * planes_written is how many destination planes a frame call fills: 3 for an
+ * RGB output, num_planes with the flexible protocol (plane c = channel c: the
+ * adapter stores plane 0 in the frame and each plane as MlrtFlexible<c>), else
+ * 1. in_fp32 / out_fp32 give the engine's boundary types after the load-time
+ * fp16 conversion. A frame of w x h comes out as (w * scale_w) x (h * scale_h). */
+typedef struct arthip_vs_model_info {
+  arthip_vs_format format;
+  int width;
+  int height;
+  int num_planes;
+  int planes_written;
+  int flexible;
+  int in_fp32;
+  int out_fp32;
+  int num_streams;
+  int scale_w;
+  int scale_h;
+} arthip_vs_model_info;
+
+/* hipCreate (vs_hip.cpp:401-591): validates the clip format and the
+ * arguments, loads the model (fp16 != 0, the default, applies the fp32 ->
+ * fp16 model conversion), builds num_streams engines and describes the output
+ * clip. width / height are the clip's. No device work happens here. Returns 1
+ * with the error text on any refusal. */
+int arthip_vs_model_create(const arthip_vs_model_args* args, int num_clips,
+                           const arthip_vs_format* clip_format, int width, int height,
+                           arthip_vs_model** out, arthip_vs_model_info* info, char* err,
+                           int errlen);
+
+/* hipGetFrame (vs_hip.cpp:77-385): one frame. fmt is the frame's format;
+ * plane_w / plane_h / src / src_stride (bytes) have fmt->num_planes entries;
+ * dst / dst_stride have n_dst >= planes_written entries, each an
+ * info.width x info.height plane of info.format samples. Thread-safe; each
+ * call runs on an idle engine of the pool, or waits for one. Returns 2 on
+ * failure. */
+int arthip_vs_model_get_frame(arthip_vs_model* model, const arthip_vs_format* fmt,
+                              const int* plane_w, const int* plane_h, const void* const* src,
+                              const ptrdiff_t* src_stride, void* const* dst,
+                              const ptrdiff_t* dst_stride, int n_dst, char* err, int errlen);
+
+void arthip_vs_model_destroy(arthip_vs_model* model);
+
+/* hip.Version (vs_hip.cpp:597-603): the library version and, when the HIP
+ * runtime answers, the device count (else *device_count = -1). */
+int arthip_vs_version(char* version, int len, int* device_count);
+
+/* hip.DeviceProperties (vs_hip.cpp:605-617). Returns 1 with
+ * "hipDeviceProperties: failed to query device" when the query fails. */
+int arthip_vs_device_properties(int device_id, char* name, int namelen, int64_t* pci_device_id,
+                                int64_t* clock_rate, int64_t* global_memory, char* err,
+                                int errlen);
+
+/* ------------------------------------------------------------------------ */
 /* Kernel-level entry points (one fused conv on device buffers)              */
 /* ------------------------------------------------------------------------ */
 
@@ -152,6 +251,12 @@ int arthip_conv3x3_limits(int* max_c, int* max_m);
  * (HipEngine::FloatToHalfBitsRNE / HalfBitsToFloat, hip_engine.h:108-109). */
 uint16_t arthip_f32_to_f16(float f);
 float arthip_f16_to_f32(uint16_t h);
+
+/* fp32 -> fp16 with the load-time model converter's rounding
+ * (src/vapoursynth/convert_float_to_float16.cpp:158-186), which the
+ * VapourSynth filter applies to fp32 initializers with fp16=1: nearest even,
+ * but |f| < 2^-14 becomes a signed zero and NaN a signed inf. */
+uint16_t arthip_f32_to_f16_no_subnormals(float f);
 
 /* Thread-local text of the last failure of a kernel-level call. */
 const char* arthip_last_error(void);
