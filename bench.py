@@ -53,6 +53,10 @@ def parse():
                    help="rows of the frame in the CPU baseline sample (0 disables it)")
     p.add_argument("--no-profile", action="store_true",
                    help="skip the per-launch event timing (roofline becomes null)")
+    p.add_argument("--host-path", type=int, default=0, metavar="STREAMS",
+                   help="instead of the device-resident bench, time the VapourSynth filter "
+                        "path (host planes in and out, PCIe included) with STREAMS engines and "
+                        "STREAMS + 1 caller threads; prints its own JSON line")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="instead of the bench, run a plain device copy of MB megabytes "
                         "(--steps times): the known-traffic kernel that scales rocprofv3 "
@@ -99,6 +103,52 @@ def cpu_baseline(spec, x_full, rows: int) -> dict | None:
     }
 
 
+def host_path(args) -> int:
+    """Frames/s through arthip_vs_model_get_frame: fp16 planes in host memory
+    (GRAYH), copied to pinned staging, uploaded, run, downloaded and copied
+    into the caller's output plane, from several threads over an engine pool."""
+    import threading
+
+    from arthip_amd import models, vs
+    from arthip_amd import onnx_proto as op
+
+    builder = {"r8f64": models.r8f64, "r16f96": models.r16f96, "c4f32": models.c4f32}[args.model]
+    spec = builder(seed=0)
+    h, w = args.height, args.width
+    frame = models.synthetic_input((1, 1, h, w), seed=1)[0, 0]
+    streams = args.host_path
+    threads = streams + 1
+    with vs.Model("GRAYH", w, h, op.encode_model(spec.model), num_streams=streams) as m:
+        for _ in range(max(args.warmup, threads)):
+            m.get_frame([frame])
+        counter = iter(range(args.steps))
+        lock = threading.Lock()
+
+        def work():
+            while True:
+                with lock:
+                    if next(counter, None) is None:
+                        return
+                m.get_frame([frame])
+
+        pool = [threading.Thread(target=work) for _ in range(threads)]
+        t0 = time.perf_counter()
+        for t in pool:
+            t.start()
+        for t in pool:
+            t.join()
+        wall = time.perf_counter() - t0
+    print(json.dumps({
+        "metric": f"frames/sec @{w}x{h} {spec.name} through the VapourSynth filter path "
+                  "(host planes in and out, PCIe included)",
+        "value": round(args.steps / wall, 3), "unit": "frames/s", "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(1000 * wall / args.steps, 4),
+        "num_streams": streams, "threads": threads, "clip_format": "GRAYH",
+        "data": "synthetic (seeded He-normal fp16 weights, uniform[0,1) luma)",
+    }), flush=True)
+    return 0
+
+
 def stream_copy_gbs(nbytes: int, reps: int = 20) -> float:
     """Read + write GB/s of a device-to-device copy of nbytes (best of reps)."""
     import torch
@@ -135,6 +185,8 @@ def main() -> int:
     args = parse()
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy, args.steps)
+    if args.host_path:
+        return host_path(args)
     if args.gpus != 1:
         print(f"bench.py: measures one GPU only; --gpus {args.gpus} is not supported "
               "(frames are independent: several GPUs would each run whole frames)",
