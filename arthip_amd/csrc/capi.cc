@@ -9,6 +9,7 @@
 #include "arthip.h"
 #include "clip.h"
 #include "engine.h"
+#include "ep.h"
 #include "half.h"
 #include "launch.h"
 #include "pack.h"
@@ -273,6 +274,62 @@ int engine_alloc_failure_then_run(const char* model_path, int N, int bigH, int b
   if (out_fp32) *out_fp32 = eng->OutputFp32() ? 1 : 0;
   write_shape(o, out_shape, out_rank);
   copy_out("", runerr, runerrlen);
+  return ARTHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// ONNX Runtime execution provider
+// ---------------------------------------------------------------------------
+
+int arthip_ep_get_capability(const void* model, size_t size, int device_id, int* n_runs,
+                             int* run_start, int max_runs, int* n_nodes, int* nodes,
+                             int max_nodes, char* err, int errlen) {
+  if (n_runs) *n_runs = 0;
+  if (n_nodes) *n_nodes = 0;
+  if (model == nullptr || n_runs == nullptr || n_nodes == nullptr)
+    return report("null model or output count", ARTHIP_ERR_BUILD, err, errlen);
+  if (device_id >= 0) {
+    // Context initialization (hip_execution_provider.cc:163-176): a device that
+    // cannot be selected and initialized gets no nodes.
+    if (hipSetDevice(device_id) != hipSuccess || hipFree(nullptr) != hipSuccess) {
+      (void)hipGetLastError();
+      copy_out("", err, errlen);
+      return ARTHIP_OK;
+    }
+  }
+  arthip::onnx::Model m;
+  std::string e;
+  if (!arthip::onnx::ParseModel(model, size, m, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  std::vector<arthip::EpRun> runs;
+  if (!arthip::EpPartition(m, runs, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  int total = 0;
+  for (const auto& r : runs) total += static_cast<int>(r.nodes.size());
+  *n_runs = static_cast<int>(runs.size());
+  *n_nodes = total;
+  if (static_cast<int>(runs.size()) + 1 > max_runs || total > max_nodes || run_start == nullptr ||
+      (total > 0 && nodes == nullptr))
+    return report("capability output arrays are too small", ARTHIP_ERR_BUILD, err, errlen);
+  int k = 0;
+  for (size_t r = 0; r < runs.size(); ++r) {
+    run_start[r] = k;
+    for (int i : runs[r].nodes) nodes[k++] = i;
+  }
+  run_start[runs.size()] = k;
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
+int arthip_engine_build_subgraph(arthip_engine* eng, const void* model, size_t size,
+                                 const int* nodes, int n_nodes, char* err, int errlen) {
+  if (eng == nullptr || model == nullptr || (n_nodes > 0 && nodes == nullptr))
+    return report("null engine, model or node list", ARTHIP_ERR_BUILD, err, errlen);
+  arthip::onnx::Model m, sub;
+  std::string e;
+  if (!arthip::onnx::ParseModel(model, size, m, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  const std::vector<int> run(nodes, nodes + (n_nodes > 0 ? n_nodes : 0));
+  if (!arthip::EpRunModel(m, run, sub, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  if (!eng->eng->BuildParsed(sub, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  copy_out("", err, errlen);
   return ARTHIP_OK;
 }
 

@@ -87,6 +87,15 @@ bool Engine::BuildFile(const std::string& path, std::string& error, const BuildO
   return true;
 }
 
+bool Engine::BuildParsed(const onnx::Model& model, std::string& error, const BuildOptions& opts) {
+  std::lock_guard<std::mutex> lock(mu_);
+  FreeAll();
+  built_ = false;
+  if (!BuildGraph(model, graph_, error, opts)) return false;
+  built_ = true;
+  return true;
+}
+
 int Engine::InputChannels() const {
   for (const Op& op : graph_.ops)
     if (op.kind == OpKind::Conv) return static_cast<int>(graph_.weights.at(op.weight).dims[1]);

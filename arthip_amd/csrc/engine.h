@@ -68,6 +68,8 @@ class Engine {
              const BuildOptions& opts = BuildOptions());
   bool BuildFile(const std::string& path, std::string& error,
                  const BuildOptions& opts = BuildOptions());
+  bool BuildParsed(const onnx::Model& model, std::string& error,
+                   const BuildOptions& opts = BuildOptions());
 
   bool OutputShape(const int64_t in_nchw[4], int64_t out_nchw[4]) const;
   bool InputFp32() const { return graph_.input_fp32; }

@@ -62,7 +62,7 @@ class Reader {
   }
 
   bool skip(uint32_t wire) {
-    uint64_t v;
+    uint64_t v = 0;
     uint32_t v32;
     const uint8_t* b;
     size_t n;
@@ -105,7 +105,7 @@ class Reader {
 template <typename T>
 bool ReadRepeatedVarint(Reader& r, uint32_t wire, std::vector<T>& out) {
   if (wire == kVarint) {
-    uint64_t v;
+    uint64_t v = 0;
     if (!r.varint(v)) return false;
     out.push_back(static_cast<T>(static_cast<int64_t>(v)));
     return true;
@@ -115,7 +115,7 @@ bool ReadRepeatedVarint(Reader& r, uint32_t wire, std::vector<T>& out) {
   Reader s = r.sub(ok);
   if (!ok) return false;
   while (!s.done()) {
-    uint64_t v;
+    uint64_t v = 0;
     if (!s.varint(v)) return r.fail();
     out.push_back(static_cast<T>(static_cast<int64_t>(v)));
   }
@@ -129,7 +129,7 @@ bool ReadRepeatedFloat(Reader& r, uint32_t wire, std::vector<float>& out) {
     out.push_back(f);
   };
   if (wire == kFixed32) {
-    uint32_t v;
+    uint32_t v = 0;
     if (!r.fixed32(v)) return false;
     put(v);
     return true;
@@ -139,7 +139,7 @@ bool ReadRepeatedFloat(Reader& r, uint32_t wire, std::vector<float>& out) {
   Reader s = r.sub(ok);
   if (!ok) return false;
   while (!s.done()) {
-    uint32_t v;
+    uint32_t v = 0;
     if (!s.fixed32(v)) return r.fail();
     put(v);
   }
@@ -153,7 +153,7 @@ bool ReadRepeatedDouble(Reader& r, uint32_t wire, std::vector<double>& out) {
     out.push_back(d);
   };
   if (wire == kFixed64) {
-    uint64_t v;
+    uint64_t v = 0;
     if (!r.fixed64(v)) return false;
     put(v);
     return true;
@@ -163,7 +163,7 @@ bool ReadRepeatedDouble(Reader& r, uint32_t wire, std::vector<double>& out) {
   Reader s = r.sub(ok);
   if (!ok) return false;
   while (!s.done()) {
-    uint64_t v;
+    uint64_t v = 0;
     if (!s.fixed64(v)) return r.fail();
     put(v);
   }
@@ -178,7 +178,7 @@ bool ParseTensor(Reader r, Tensor& t) {
     switch (f) {
       case 1: ok = ReadRepeatedVarint(r, w, t.dims); break;
       case 2: {
-        uint64_t v;
+        uint64_t v = 0;
         ok = w == kVarint && r.varint(v);
         t.data_type = static_cast<int32_t>(v);
         break;
@@ -194,7 +194,7 @@ bool ParseTensor(Reader r, Tensor& t) {
         ok = r.skip(w);
         break;
       case 14: {
-        uint64_t v;
+        uint64_t v = 0;
         ok = w == kVarint && r.varint(v);
         t.data_location = static_cast<int32_t>(v);
         break;
@@ -214,20 +214,20 @@ bool ParseAttribute(Reader r, Attribute& a) {
     switch (f) {
       case 1: ok = w == kLen && r.string(a.name); break;
       case 20: {
-        uint64_t v;
+        uint64_t v = 0;
         ok = w == kVarint && r.varint(v);
         a.type = static_cast<int32_t>(v);
         break;
       }
       case 2: {
-        uint32_t v;
+        uint32_t v = 0;
         ok = w == kFixed32 && r.fixed32(v);
         std::memcpy(&a.f, &v, 4);
         a.has_f = true;
         break;
       }
       case 3: {
-        uint64_t v;
+        uint64_t v = 0;
         ok = w == kVarint && r.varint(v);
         a.i = static_cast<int64_t>(v);
         a.has_i = true;
@@ -299,7 +299,7 @@ bool ParseDim(Reader r, int64_t& dim) {
     if (!r.key(f, w)) return false;
     bool ok = true;
     if (f == 1 && w == kVarint) {
-      uint64_t v;
+      uint64_t v = 0;
       ok = r.varint(v);
       dim = static_cast<int64_t>(v);
     } else {
@@ -336,7 +336,7 @@ bool ParseTensorType(Reader r, ValueInfo& vi) {
     if (!r.key(f, w)) return false;
     bool ok = true;
     if (f == 1 && w == kVarint) {
-      uint64_t v;
+      uint64_t v = 0;
       ok = r.varint(v);
       vi.elem_type = static_cast<int32_t>(v);
     } else if (f == 2 && w == kLen) {
@@ -432,7 +432,7 @@ bool ParseOpset(Reader r, OpsetId& o) {
     if (f == 1 && w == kLen) {
       ok = r.string(o.domain);
     } else if (f == 2 && w == kVarint) {
-      uint64_t v;
+      uint64_t v = 0;
       ok = r.varint(v);
       o.version = static_cast<int64_t>(v);
     } else {
@@ -466,7 +466,7 @@ bool ParseModel(const void* data, size_t size, Model& model, std::string& error)
     bool sok = true;
     switch (f) {
       case 1: {
-        uint64_t v;
+        uint64_t v = 0;
         ok = w == kVarint && r.varint(v);
         model.ir_version = static_cast<int64_t>(v);
         break;

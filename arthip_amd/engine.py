@@ -29,6 +29,41 @@ class EngineError(RuntimeError):
     """The engine rejected the model, the shape, or the run."""
 
 
+def model_bytes(model) -> bytes:
+    """Serialized ONNX bytes of a path, bytes, onnx_proto.Model or models.ModelSpec."""
+    if isinstance(model, (str, Path)):
+        return Path(model).read_bytes()
+    if hasattr(model, "bytes") and callable(model.bytes):
+        return model.bytes()
+    if hasattr(model, "graph"):
+        from .onnx_proto import encode_model
+        return encode_model(model)
+    return bytes(model)
+
+
+def get_capability(model, device_id: int = -1) -> list[list[int]]:
+    """The ONNX Runtime EP's GetCapability: node indices of each claimed run.
+    device_id >= 0 claims nothing when that device cannot be initialized."""
+    lib = _lib.lib()
+    data = model_bytes(model)
+    buf = ctypes.create_string_buffer(data, len(data))
+    n_runs, n_nodes = ctypes.c_int(), ctypes.c_int()
+    cap_r, cap_n = 64, 4096
+    for _ in range(2):
+        starts = (ctypes.c_int * (cap_r + 1))()
+        nodes = (ctypes.c_int * cap_n)()
+        e = _err()
+        rc = lib.arthip_ep_get_capability(buf, len(data), device_id, ctypes.byref(n_runs), starts,
+                                          cap_r + 1, ctypes.byref(n_nodes), nodes, cap_n, e,
+                                          _ERR_LEN)
+        if rc == 0:
+            return [list(nodes[starts[r]:starts[r + 1]]) for r in range(n_runs.value)]
+        if n_runs.value + 1 <= cap_r + 1 and n_nodes.value <= cap_n:
+            raise EngineError(_msg(e, f"get_capability failed (rc={rc})"))
+        cap_r, cap_n = n_runs.value, max(n_nodes.value, 1)
+    raise EngineError(_msg(e, "get_capability failed"))
+
+
 def _err() -> ctypes.Array:
     return ctypes.create_string_buffer(_ERR_LEN)
 
@@ -76,15 +111,22 @@ class Engine:
         if isinstance(model, (str, Path)):
             rc = self._lib.arthip_engine_build_file(self._h, str(model).encode(), e, _ERR_LEN)
         else:
-            if hasattr(model, "bytes") and callable(model.bytes):
-                data = model.bytes()
-            elif hasattr(model, "graph"):
-                from .onnx_proto import encode_model
-                data = encode_model(model)
-            else:
-                data = bytes(model)
+            data = model_bytes(model)
             buf = ctypes.create_string_buffer(data, len(data))
             rc = self._lib.arthip_engine_build_bytes(self._h, buf, len(data), e, _ERR_LEN)
+        if rc != 0:
+            raise EngineError(_msg(e, f"build failed (rc={rc})"))
+        return self
+
+    def build_subgraph(self, model, nodes) -> "Engine":
+        """The ONNX Runtime EP's Compile for one claimed run: the engine runs the
+        given nodes (indices in graph order) of the model."""
+        data = model_bytes(model)
+        buf = ctypes.create_string_buffer(data, len(data))
+        idx = (ctypes.c_int * max(len(nodes), 1))(*nodes)
+        e = _err()
+        rc = self._lib.arthip_engine_build_subgraph(self._h, buf, len(data), idx, len(nodes), e,
+                                                    _ERR_LEN)
         if rc != 0:
             raise EngineError(_msg(e, f"build failed (rc={rc})"))
         return self

@@ -87,6 +87,30 @@ int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_
                                int errlen);
 
 /* ------------------------------------------------------------------------ */
+/* ONNX Runtime execution provider: partitioning and compile                  */
+/* ------------------------------------------------------------------------ */
+
+/* GetCapability (src/onnxruntime-hip/hip_execution_provider.cc:181-335 with
+ * IsNodeSupported 22-177): the maximal runs of consecutive supported nodes
+ * of a serialized model, keeping only runs with one activation input and one
+ * needed output. Run r is nodes[run_start[r] .. run_start[r+1]) (node indices
+ * in graph order). device_id >= 0 first initializes that device and claims
+ * nothing (*n_runs = 0, return 0) when it cannot (the reference's refusal after
+ * a failed context init); device_id < 0 skips the device. Returns 1 on a
+ * malformed model or when max_runs + 1 / max_nodes entries do not suffice (then
+ * *n_runs and *n_nodes still give the sizes needed). Supported beyond the
+ * reference: Relu. Refused beyond it: a Conv over the engine's channel limits. */
+int arthip_ep_get_capability(const void* model, size_t size, int device_id, int* n_runs,
+                             int* run_start, int max_runs, int* n_nodes, int* nodes,
+                             int max_nodes, char* err, int errlen);
+
+/* Compile for one claimed run (hip_execution_provider.cc:337-357): builds the
+ * engine from the run's nodes of the serialized model, with the run's single
+ * activation as input 0 and its single output as output 0. */
+int arthip_engine_build_subgraph(arthip_engine* eng, const void* model, size_t size,
+                                 const int* nodes, int n_nodes, char* err, int errlen);
+
+/* ------------------------------------------------------------------------ */
 /* Test-driver ABI: same names, arguments and return codes as the reference's */
 /* ctypes driver (tests/correctness/harness/engine_harness.cc:56-210). Each   */
 /* call builds a fresh engine from a model file.                              */

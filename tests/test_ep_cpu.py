@@ -1,0 +1,203 @@
+"""The ONNX Runtime execution provider's partitioning without a GPU
+(arthip_ep_get_capability with no device check).
+
+Mirrors the reference's capability rules (src/onnxruntime-hip/
+hip_execution_provider.cc:22-177 IsNodeSupported, 181-335 GetCapability) and
+the cases its EP tests drive through ONNX Runtime (tests/correctness/
+test_ep.py): the fp32-boundary conv fixture is claimed whole (P1-4), a region
+with two activation inputs is not claimed (P2-17), a graph input shared by two
+convs is one deduplicated input (P2-17). ONNX Runtime is not installed, so the
+partition is checked directly, node by node.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from arthip_amd import onnx_proto as op
+from arthip_amd.engine import EngineError, get_capability
+from tests.fixtures import _conv, _half, _model, kern, linspace
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+F16, F32 = op.FLOAT16, op.FLOAT
+
+
+def conv_model(*, c=4, m=4, k=3, extra=None, bias_dtype=np.float16, **conv_attrs):
+    """One Conv node (weights from an initializer) with attribute overrides."""
+    w = kern(21, m, c, k)
+    attrs = dict(kernel_shape=[k, k], pads=[1, 1, 1, 1], strides=[1, 1], dilations=[1, 1],
+                 group=1)
+    attrs.update(conv_attrs)
+    attrs = {a: v for a, v in attrs.items() if v is not None}
+    node = op.node("Conv", ["x", "w", "b"], ["y"], **attrs)
+    b = linspace(m).astype(bias_dtype)
+    inits = [_half("w", w), op.tensor("b", b)]
+    return _model([node] + (extra or []), "x", [1, c, "h", "w"], F16, "y", [1, m, "h", "w"], F16,
+                  inits)
+
+
+def claims(model):
+    return get_capability(model)
+
+
+# ---------------------------------------------------------------------------
+# Whole-model claims and the single-input / single-output rule
+# ---------------------------------------------------------------------------
+
+def test_fp32_boundary_conv_is_claimed_whole(fixtures):
+    assert claims(fixtures.get("ep_conv_fp32io").model) == [[0, 1, 2]]
+
+
+def test_two_activation_inputs_are_not_claimed():
+    g = op.Graph(nodes=[op.node("Add", ["x1", "x2"], ["y"])],
+                 inputs=[op.value_info("x1", F16, [1, 4, "h", "w"]),
+                         op.value_info("x2", F16, [1, 4, "h", "w"])],
+                 outputs=[op.value_info("y", F16, [1, 4, "h", "w"])])
+    assert claims(op.Model(graph=g)) == []
+
+
+def test_shared_graph_input_is_deduplicated(fixtures):
+    assert claims(fixtures.get("ep_two_convs_one_input").model) == [[0, 1, 2]]
+
+
+def test_shipped_luma_model_is_claimed_whole():
+    m = op.load(GOLDEN / "ArtCNN_R8F64_fp16.onnx")
+    assert claims(m) == [list(range(len(m.graph.nodes)))]
+
+
+def test_fp32_model_is_not_claimed_but_its_fp16_conversion_is():
+    from oracle.convert import to_fp16
+    m = op.load(GOLDEN / "ArtCNN_R8F64_Chroma.onnx")
+    assert claims(m) == []
+    conv = to_fp16(m, cast_input=True, cast_output=True)
+    assert claims(conv) == [list(range(len(conv.graph.nodes)))]
+
+
+def test_unsupported_node_splits_the_graph():
+    w1, w2 = kern(31, 4, 4), kern(32, 4, 4)
+    nodes = [_conv("x", "w1", None, "a"),
+             op.node("Cast", ["a"], ["a32"], to=F32),    # not at a graph output
+             op.node("Cast", ["a32"], ["a16"], to=F16),  # not from a graph input
+             _conv("a16", "w2", None, "y")]
+    m = _model(nodes, "x", [1, 4, "h", "w"], F16, "y", [1, 4, "h", "w"], F16,
+               [_half("w1", w1), _half("w2", w2)])
+    assert claims(m) == [[0], [3]]
+
+
+def test_output_needed_outside_the_run_blocks_the_claim():
+    w1, w2 = kern(33, 4, 4), kern(34, 4, 4)
+    nodes = [_conv("x", "w1", None, "a"), _conv("a", "w2", None, "b"),
+             op.node("Cast", ["b"], ["b32"], to=F32), op.node("Cast", ["b32"], ["c"], to=F16),
+             op.node("Add", ["a", "c"], ["y"])]
+    m = _model(nodes, "x", [1, 4, "h", "w"], F16, "y", [1, 4, "h", "w"], F16,
+               [_half("w1", w1), _half("w2", w2)])
+    # Run [0, 1] exports both a and b; run [4] reads two activations.
+    assert claims(m) == []
+
+
+def test_graph_output_consumed_inside_is_still_exported():
+    w1, w2 = kern(35, 4, 4), kern(36, 4, 4)
+    nodes = [_conv("x", "w1", None, "a"), _conv("a", "w2", None, "y")]
+    g = op.Graph(nodes=nodes, initializers=[_half("w1", w1), _half("w2", w2)],
+                 inputs=[op.value_info("x", F16, [1, 4, "h", "w"])],
+                 outputs=[op.value_info("y", F16, [1, 4, "h", "w"]),
+                          op.value_info("a", F16, [1, 4, "h", "w"])])
+    assert claims(op.Model(graph=g)) == []  # two needed outputs
+
+
+def test_nodes_out_of_topological_order_are_an_error():
+    w1, w2 = kern(37, 4, 4), kern(38, 4, 4)
+    nodes = [_conv("a", "w2", None, "y"), _conv("x", "w1", None, "a")]
+    m = _model(nodes, "x", [1, 4, "h", "w"], F16, "y", [1, 4, "h", "w"], F16,
+               [_half("w1", w1), _half("w2", w2)])
+    with pytest.raises(EngineError, match="topological"):
+        claims(m)
+
+
+# ---------------------------------------------------------------------------
+# IsNodeSupported, node by node
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("attrs,claimed", [
+    (dict(), True),
+    (dict(pads=[1, 0, 1, 0]), False),          # asymmetric: another convolution
+    (dict(pads=[0, 0, 0, 0]), False),
+    (dict(pads=None), False),                  # no padding at all
+    (dict(pads=None, auto_pad="SAME_UPPER"), True),
+    (dict(pads=None, auto_pad="SAME_LOWER"), True),
+    (dict(pads=None, auto_pad="VALID"), False),
+    (dict(auto_pad="NOTSET"), True),
+    (dict(strides=[2, 2]), False),
+    (dict(dilations=[2, 2]), False),
+    (dict(group=2), False),
+], ids=["plain", "pads-1010", "pads-0", "no-pads", "same-upper", "same-lower", "valid",
+        "notset", "stride2", "dilation2", "group2"])
+def test_conv_attributes(attrs, claimed):
+    assert bool(claims(conv_model(**attrs))) == claimed
+
+
+def test_conv_kernel_and_dtype_rules():
+    assert claims(conv_model(k=5, kernel_shape=[5, 5], pads=[2, 2, 2, 2])) == []
+    assert claims(conv_model(bias_dtype=np.float32)) == []          # fp16 tensors only
+    assert claims(conv_model(c=97, m=4)) == []                      # beyond the engine's C limit
+    assert claims(conv_model(c=4, m=129)) == []                     # beyond its M limit
+    assert claims(conv_model(c=96, m=128)) == [[0]]
+
+
+def test_weight_must_be_an_initializer():
+    g = op.Graph(nodes=[op.node("Conv", ["x", "w"], ["y"], kernel_shape=[3, 3],
+                                pads=[1, 1, 1, 1])],
+                 inputs=[op.value_info("x", F16, [1, 4, "h", "w"]),
+                         op.value_info("w", F16, [4, 4, 3, 3])],
+                 outputs=[op.value_info("y", F16, [1, 4, "h", "w"])])
+    assert claims(op.Model(graph=g)) == []
+
+
+def _tail(node, inits=(), inputs=None):
+    """conv -> node, the node's output the graph output."""
+    w = kern(41, 4, 4)
+    nodes = [_conv("x", "w", None, "a"), node]
+    return _model(nodes, "x", [1, 4, "h", "w"], F16, node.outputs[0], [1, 4, "h", "w"], F16,
+                  [_half("w", w)] + list(inits), inputs=inputs)
+
+
+def test_depth_to_space_rules():
+    assert claims(_tail(op.node("DepthToSpace", ["a"], ["y"], blocksize=2, mode="DCR"))) == [[0, 1]]
+    assert claims(_tail(op.node("DepthToSpace", ["a"], ["y"], blocksize=2))) == [[0, 1]]
+    assert claims(_tail(op.node("DepthToSpace", ["a"], ["y"], blocksize=2, mode="CRD"))) == [[0]]
+    assert claims(_tail(op.node("DepthToSpace", ["a"], ["y"], blocksize=0))) == [[0]]
+
+
+def test_clip_bounds_must_be_initializers():
+    lo, hi = op.tensor("lo", np.float16(0.0)), op.tensor("hi", np.float16(1.0))
+    assert claims(_tail(op.node("Clip", ["a", "lo", "hi"], ["y"]), [lo, hi])) == [[0, 1]]
+    assert claims(_tail(op.node("Clip", ["a", "", "hi"], ["y"]), [hi])) == [[0, 1]]
+    dyn = [op.value_info("x", F16, [1, 4, "h", "w"]), op.value_info("hi", F16, [])]
+    assert claims(_tail(op.node("Clip", ["a", "lo", "hi"], ["y"]), [lo], inputs=dyn)) == [[0]]
+
+
+def test_relu_and_domains():
+    assert claims(_tail(op.node("Relu", ["a"], ["y"]))) == [[0, 1]]
+    custom = op.node("Relu", ["a"], ["y"])
+    custom.domain = "com.example"
+    assert claims(_tail(custom)) == [[0]]
+    assert claims(_tail(op.node("Tanh", ["a"], ["y"]))) == [[0]]
+
+
+def test_boundary_casts_only():
+    w = kern(42, 1, 1)
+    inner = [op.node("Cast", ["x"], ["x16"], to=F16), _conv("x16", "w", None, "a"),
+             op.node("Cast", ["a"], ["y"], to=F32)]
+    m = _model(inner, "x", [1, 1, "h", "w"], F32, "y", [1, 1, "h", "w"], F32, [_half("w", w)])
+    assert claims(m) == [[0, 1, 2]]
+    # A Cast to fp16 whose input is not a graph input is not a boundary Cast.
+    w2 = kern(43, 1, 1)
+    mid = [op.node("Cast", ["x"], ["x16"], to=F16), _conv("x16", "w", None, "a"),
+           op.node("Cast", ["a"], ["a32"], to=F32), op.node("Cast", ["a32"], ["b"], to=F16),
+           _conv("b", "w2", None, "c"), op.node("Cast", ["c"], ["y"], to=F32)]
+    m2 = _model(mid, "x", [1, 1, "h", "w"], F32, "y", [1, 1, "h", "w"], F32,
+                [_half("w", w), _half("w2", w2)])
+    assert claims(m2) == [[0, 1], [4, 5]]
