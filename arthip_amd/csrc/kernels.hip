@@ -846,21 +846,23 @@ winograd_strip(StripArgs a) {
 // winograd_strip, split over two kinds of waves of one 512-thread workgroup
 // per CU:
 //   * waves 0 .. 2*KC-1 (consumers) keep U' of 16 output channels each in
-//     VGPRs, run the MFMA fold and the activation into staging, and move the
-//     staged outputs of the item before to HBM;
+//     VGPRs and run the MFMA fold into staging;
 //   * the other waves (producers) load input rows and write V'. Holding no U',
 //     they keep PipeL<KC>::NW - 1 row pairs in flight ahead of the transform,
 //     so HBM latency hides behind that many items of work.
-// Step j (one barrier each): the producers transform item j; the consumers
-// store item j-2 and fold item j-1. V' and staging are double-buffered by item
-// parity, so each buffer's writes and reads are a barrier apart. A run (the
-// items of one strip) restarts the producers' row window.
+// Step j (one barrier each): the producers transform item j, the consumers
+// fold item j-1, and item j-2 leaves staging for HBM. V' and staging are
+// double-buffered by item parity, so each buffer's writes and reads are a
+// barrier apart. A run (the items of one strip) restarts the producers' row
+// window.
 //
-// Residual inputs: the producers load item j's residual tile in step j (ahead
-// of their row prefetch, so that waiting for it leaves the prefetch in flight)
-// and write it in step j+1 to a double-buffered LDS tile in the staging layout
-// (two inputs are added there in fp16, s0 + s1); the consumers add it to the
-// staged output when they store the item in step j+2.
+// Who moves item j-2 to HBM depends on C. At C = 64 the consumers apply the
+// activation in the fold and store (four producer waves, one task each, have
+// no room for it: 138 us instead of 122 with producer stores). At C = 96 the
+// six consumer waves are the critical path, so the producers take the store
+// phase: activation on the staged fp16 values, the residual inputs (loaded into
+// registers one step ahead, added in graph order) and the stores. That took
+// the one-residual 96 -> 96 layer from 312 to 279 us.
 //
 // Measured on the 1080p 64 -> 64 ReLU conv: 145 us with winograd_strip, 122 us
 // here. Items of 32 tiles (two MFMA column blocks per wave) ran at 146 us: at
@@ -905,11 +907,24 @@ struct PipeLds {
   static constexpr int NCW = 2 * KC;        // consumer waves
   static constexpr int NPT = 64 * (8 - NCW);  // producer threads
   static constexpr int UP = 16 * 8 * KC / NPT;  // producer tasks per thread
-  static constexpr int SKC = 2 * PXS * (C / 8) / NPT;  // residual chunks per producer thread
-  static constexpr size_t lds_bytes(int nskip) {
-    return (size_t)2 * (VBUF + SBUF + (nskip > 0 ? SBUF : 0)) * 2;
-  }
+  static constexpr int OCH = 2 * PXS * (C / 8) / NPT;  // 16-byte output chunks per producer thread
+  static constexpr size_t lds_bytes() { return (size_t)2 * (VBUF + SBUF) * 2; }
 };
+
+// Activation of 8 fp16 values, each computed from the fp16 value in fp32 and
+// rounded back (the same arithmetic as strip_act4 after its rounding).
+template <int ACT>
+__device__ __forceinline__ h8 act8(h8 r) {
+  if (ACT == kActRelu) r = __builtin_elementwise_max(r, h8{0, 0, 0, 0, 0, 0, 0, 0});
+  if (ACT == kActSilu) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (float)r[e];
+      r[e] = (_Float16)(x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)));
+    }
+  }
+  return r;
+}
 
 template <int KC, int ACT, int NSKIP>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -927,11 +942,17 @@ winograd_pipe(StripArgs a) {
   constexpr int GR = C / 8;  // 16-byte groups per pixel
   constexpr int QUADS = C / 4;
   constexpr int PX = 2 * C;
+  constexpr int OCH = L::OCH;
+  // Who stores: the producers at C = 96 (six consumer waves are the critical
+  // path there), the consumers at C = 64 (one producer wave per SIMD has no
+  // room for the store phase).
+  constexpr bool PS = KC == 3;
+  static_assert(PS || NSKIP == 0, "residual inputs go through the producer store");
   static_assert(L::NPT * UP == 16 * QUADS, "producer tasks cover the item");
-  // 2 V' | 2 staging | 2 residual tiles (with residual inputs)
+  static_assert(L::NPT * OCH == 2 * PXS * GR, "producer stores cover the item");
+  // 2 V' | 2 staging
   extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
   _Float16* const stg = vlds + 2 * VBUF;
-  _Float16* const skt = stg + 2 * SBUF;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -947,8 +968,7 @@ winograd_pipe(StripArgs a) {
   const uint32_t rb32 = (uint32_t)row_bytes;
   const int n_rec = (int)(rb32 + L::PXS * PX);  // bytes of an item's two output rows
   constexpr uint32_t kOob = 0x80000000u;
-  int n, s, th;
-  auto decode = [&](int item) {
+  auto decode = [&](int item, int& n, int& s, int& th) {
     const uint32_t sgl = fdiv((uint32_t)item, a.fd_tiles_h);
     th = item - (int)(sgl * (uint32_t)a.tiles_h);
     const uint32_t nn = fdiv(sgl, a.fd_strips);
@@ -957,7 +977,7 @@ winograd_pipe(StripArgs a) {
   };
 
   if (wave < NCW) {
-    // ---- consumers: step j stores item j-2 and folds item j-1 -------------
+    // ---- consumers: step j folds item j-1 ----------------------------------
     h8 u[16][KC];
     {
       const h8* up = reinterpret_cast<const h8*>(a.u) + (size_t)wave * (16 * KC * 64) + lane;
@@ -975,30 +995,30 @@ winograd_pipe(StripArgs a) {
     for (int kc = 0; kc < KC; ++kc) vr0[kc] = vlds + LL::at(tcol, 32 * kc + 8 * kq);
     // Pixels 2*tcol and 2*tcol + 1 share the staging rotation.
     const int sw0 = LL::st(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
-    // Store mapping: thread handles 16-byte group sg of pixel sx in both rows.
+    // Consumer store (C = 64): thread handles 16-byte group sg of pixel sx in
+    // both rows; absent items and pixels past the edges get out-of-range
+    // offsets, so every step issues the same two stores.
     const int sx = tid / GR;
     const int sg = tid - sx * GR;
     const int sr0 = LL::st(0, sx, sg);
     const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
-
-    // Item `item` from staging buffer SB (plus its residual tile); absent items and pixels past the
-    // edges get out-of-range offsets, so every step issues the same two stores.
     auto store_item = [&](int item, bool live, int SB) {
-      decode(item);
+      int n, s, th;
+      decode(item, n, s, th);
       const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + PXS * s + 1;
       char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, n_rec, 0x00020000);
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * PXS * C);
-        if (NSKIP > 0) v += *reinterpret_cast<const h8*>(skt + SB * SBUF + sr0 + r * PXS * C);
+        const h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * PXS * C);
         const bool ok = live && (PXS * s + sx < a.W) && (r == 0 || 2 * th + 1 < a.H);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs,
                                                ok ? (uint32_t)r * rb32 + s_lane : kOob, 0,
                                                kNonTemporal);
       }
     };
+
     auto fold = [&](auto buf_tag) {
       constexpr int BUF = decltype(buf_tag)::value;
       auto mm = [&](int p, f4 acc) {
@@ -1046,33 +1066,39 @@ winograd_pipe(StripArgs a) {
           y11 -= Q;
         }
       }
+      // With producer stores the activation is theirs (on the rounded value,
+      // the same arithmetic).
+      constexpr int FA = PS ? 0 : ACT;
       _Float16* sw = stg + BUF * SBUF + sw0;
-      *reinterpret_cast<h4*>(sw) = strip_act4<ACT>(y00);
-      *reinterpret_cast<h4*>(sw + C) = strip_act4<ACT>(y01);
-      *reinterpret_cast<h4*>(sw + PXS * C) = strip_act4<ACT>(y10);
-      *reinterpret_cast<h4*>(sw + (PXS + 1) * C) = strip_act4<ACT>(y11);
+      *reinterpret_cast<h4*>(sw) = strip_act4<FA>(y00);
+      *reinterpret_cast<h4*>(sw + C) = strip_act4<FA>(y01);
+      *reinterpret_cast<h4*>(sw + PXS * C) = strip_act4<FA>(y10);
+      *reinterpret_cast<h4*>(sw + (PXS + 1) * C) = strip_act4<FA>(y11);
     };
 
-    // Step j folds item j-1 into buffer (j-1)&1 and stores item j-2 from
-    // buffer j&1. Steps alternate odd/even so both parities are static.
+    // Step j folds item j-1 into buffer (j-1)&1 and, with consumer stores,
+    // first stores item j-2 from buffer j&1. Steps alternate odd/even so both
+    // parities are static.
     lds_sync();  // step 0
     for (int j = 1;; ++j) {
-      store_item(begin + (j >= 2 ? j - 2 : 0), j >= 2, 1);  // odd j
+      if constexpr (!PS) store_item(begin + (j >= 2 ? j - 2 : 0), j >= 2, 1);  // odd j
       fold(IntC<0>{});
       lds_sync();
       if (j == K) break;
       ++j;
-      store_item(begin + j - 2, true, 0);  // even j
+      if constexpr (!PS) store_item(begin + j - 2, true, 0);  // even j
       fold(IntC<1>{});
       lds_sync();
       if (j == K) break;
     }
-    store_item(begin + K - 1, true, (K + 1) & 1);  // step K + 1
-    lds_sync();
+    if constexpr (!PS) {
+      store_item(begin + K - 1, true, (K + 1) & 1);  // step K + 1
+      lds_sync();
+    }
     return;
   }
 
-  // ---- producers: step j transforms item j ---------------------------------
+  // ---- producers: step j transforms item j and stores item j-2 ---------------
   // Task v of thread p: flat index p + NPT * v -> tile, 4-channel quad.
   const int ptid = tid - 64 * NCW;
   int tt[UP];
@@ -1085,6 +1111,7 @@ winograd_pipe(StripArgs a) {
     tq4[v] = (uint32_t)(4 * (f - tt[v] * QUADS));
     vw0[v] = vlds + LL::at(tt[v], (int)tq4[v]);
   }
+  int n, s, th;  // the item being transformed
   uint32_t in_lane[UP];
   auto in_row = [&](int r) {
     if (r > a.Hp - 2) r = a.Hp - 2;
@@ -1103,69 +1130,87 @@ winograd_pipe(StripArgs a) {
         }
   };
   int par = 0;  // parity of step j = parity of item j
+  int js = 0;   // step j
 
-  // Residual tile chunks of this thread: chunk f = ptid + NPT * i -> row,
-  // pixel, 16-byte group; LDS offset in the staging layout, lane byte offset
-  // within the item's two output rows.
-  constexpr int SKC = L::SKC;
-  int sk_lds[NSKIP > 0 ? SKC : 1];
-  uint32_t sk_off[NSKIP > 0 ? SKC : 1];
-  int sk_x[NSKIP > 0 ? SKC : 1], sk_r[NSKIP > 0 ? SKC : 1];
-  h8 skv[NSKIP > 0 ? NSKIP : 1][NSKIP > 0 ? SKC : 1];
-  if (NSKIP > 0) {
+  // Output chunks of this thread: chunk f = ptid + NPT * i -> row, pixel,
+  // 16-byte group; its offset in the staging layout and in the item's two
+  // output rows. Residual chunks use the same mapping.
+  int oc_lds[OCH];
+  uint32_t oc_off[OCH];
+  int oc_x[OCH], oc_r[OCH];
 #pragma unroll
-    for (int i = 0; i < SKC; ++i) {
-      const int f = ptid + L::NPT * i;
-      const int r = f / (PXS * GR);
-      const int x = (f / GR) % PXS;
-      const int g = f % GR;
-      sk_lds[i] = LL::st(r, x, g);
-      sk_off[i] = (uint32_t)r * rb32 + (uint32_t)(x * C + g * 8) * 2;
-      sk_x[i] = x;
-      sk_r[i] = r;
-    }
+  for (int i = 0; i < OCH; ++i) {
+    const int f = ptid + L::NPT * i;
+    const int r = f / (PXS * GR);
+    const int x = (f / GR) % PXS;
+    const int g = f % GR;
+    oc_lds[i] = LL::st(r, x, g);
+    oc_off[i] = (uint32_t)r * rb32 + (uint32_t)(x * C + g * 8) * 2;
+    oc_x[i] = x;
+    oc_r[i] = r;
   }
-  // Loads item (n, s, th)'s residual tile into skv (out-of-range offsets read
-  // zero past the edges).
-  auto load_skips = [&]() {
-    const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + PXS * s + 1;
+  // Buffer resource spanning item `item`'s two output rows in `base`, and the
+  // chunk offsets: chunks past the right or bottom edge (or of an absent item)
+  // get an offset beyond the resource, which reads as zero and drops stores,
+  // so every step issues the same memory instructions.
+  auto item_rsrc = [&](const void* base, int item) {
+    int in_, is_, ith;
+    decode(item, in_, is_, ith);
+    const int64_t pix0 = ((int64_t)in_ * a.Hp + 2 * ith + 1) * a.Wp + PXS * is_ + 1;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(base) + pix0 * PX), (short)0, n_rec, 0x00020000);
+  };
+  auto chunk_off = [&](int item, bool live, int i) {
+    int in_, is_, ith;
+    decode(item, in_, is_, ith);
+    const bool ok = live && (PXS * is_ + oc_x[i] < a.W) && (oc_r[i] == 0 || 2 * ith + 1 < a.H);
+    return ok ? oc_off[i] : kOob;
+  };
+  h8 skv[NSKIP > 0 ? NSKIP : 1][OCH];
+  // Residual chunks of item `item` (issued one step before its store).
+  auto load_skips = [&](int item, bool live) {
+    if (NSKIP == 0) return;
+    const int it = live ? item : begin;
 #pragma unroll
     for (int k = 0; k < NSKIP; ++k) {
-      const char* sb = reinterpret_cast<const char*>(k == 0 ? a.skip0 : a.skip1) + pix0 * PX;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc((void*)sb, (short)0, n_rec, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs = item_rsrc(k == 0 ? a.skip0 : a.skip1, it);
 #pragma unroll
-      for (int i = 0; i < SKC; ++i) {
-        const bool ok = (PXS * s + sk_x[i] < a.W) && (sk_r[i] == 0 || 2 * th + 1 < a.H);
+      for (int i = 0; i < OCH; ++i)
         skv[k][i] = __builtin_bit_cast(
-            h8, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? sk_off[i] : kOob, 0, kNonTemporal));
-      }
+            h8, __builtin_amdgcn_raw_buffer_load_b128(rs, chunk_off(it, live, i), 0, kNonTemporal));
     }
   };
-  // Writes the residual tile loaded in the step before to buffer SB.
-  auto write_skips = [&](int SB) {
+  // Item `item` from staging buffer SB: activation, residual inputs, store.
+  auto store_item = [&](int item, bool live, int SB) {
+    const int it = live ? item : begin;
+    const __amdgpu_buffer_rsrc_t rs = item_rsrc(a.out, it);
 #pragma unroll
-    for (int i = 0; i < SKC; ++i) {
-      h8 v = skv[0][i];
+    for (int i = 0; i < OCH; ++i) {
+      h8 v = act8<ACT>(*reinterpret_cast<const h8*>(stg + SB * SBUF + oc_lds[i]));
+      if (NSKIP > 0) v += skv[0][i];
       if (NSKIP > 1) v += skv[1][i];
-      *reinterpret_cast<h8*>(skt + SB * SBUF + sk_lds[i]) = v;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs,
+                                             chunk_off(it, live, i), 0, kNonTemporal);
     }
   };
 
   auto step = [&](h2 (&top)[UP][16], h2 (&bot)[UP][16]) {
-    if (NSKIP > 0) write_skips(par ^ 1);  // item j-1 (garbage for j == 0, never stored)
+    if constexpr (PS) {
+      store_item(begin + js - 2, js >= 2, par);  // item j-2 sits in buffer j & 1
+      load_skips(begin + js - 1, js >= 1);       // item j-1, stored next step
+    }
 #pragma unroll
     for (int v = 0; v < UP; ++v) v_transform<WPS>(vw0[v] + par * VBUF, top[v], bot[v]);
-    if (NSKIP > 0) load_skips();
     load2(top, in_row(2 * (th + NW)));
     ++th;
+    ++js;
     par ^= 1;
     lds_sync();
   };
 
   h2 W[NW][UP][16];
   for (int it = begin; it < end;) {
-    decode(it);
+    decode(it, n, s, th);
     const int len = min(end - it, a.tiles_h - th);
 #pragma unroll
     for (int v = 0; v < UP; ++v) {
@@ -1196,9 +1241,17 @@ winograd_pipe(StripArgs a) {
     rest(rest, IntC<0>{});
     it += len;
   }
-  if (NSKIP > 0) write_skips(par ^ 1);  // step K: item K-1
-  lds_sync();
-  lds_sync();  // step K + 1
+  if constexpr (PS) {
+    // Step K: store item K-2, load item K-1's residuals; the consumers fold
+    // item K-1. Step K + 1: store item K-1.
+    store_item(begin + K - 2, K >= 2, par);
+    load_skips(begin + K - 1, true);
+    lds_sync();
+    store_item(begin + K - 1, true, par ^ 1);
+  } else {
+    lds_sync();  // step K: the consumers fold item K-1
+    lds_sync();  // step K + 1: they store it
+  }
 }
 
 __device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
@@ -2184,7 +2237,7 @@ hipError_t launch_pipe(const StripArgs& a, int act, hipStream_t s) {
   StripKernel pf = act == kActRelu   ? winograd_pipe<KC, kActRelu, NSKIP>
                    : act == kActSilu ? winograd_pipe<KC, kActSilu, NSKIP>
                                      : winograd_pipe<KC, kActNone, NSKIP>;
-  const size_t lds = PipeLds<KC>::lds_bytes(NSKIP);
+  const size_t lds = PipeLds<KC>::lds_bytes();
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
