@@ -253,6 +253,20 @@ def test_pipe_tiny(c, h, w):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2])
+def test_pipe_epilogue_c64(act):
+    x, wt, b = make_case(39, 1, 64, 64, 21, 70)
+    check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"pipe64 act{act}")
+
+
+# SiLU at 64 channels: the producers apply it in place on a third staging
+# buffer, so the consumers' store trails the fold by two steps (longer tail).
+@pytest.mark.parametrize("h,w", GEOMETRY + TINY + [(360, 640)])
+def test_pipe_silu_c64(h, w):
+    x, wt, b = make_case(40, 1, 64, 64, h, w)
+    check(run_conv(x, wt, b, 2), oracle_conv(x, wt, b, 2), f"pipe64 silu {h}x{w}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
 def test_pipe_epilogue_c96(act):
     x, wt, b = make_case(32, 1, 96, 96, 21, 70)
     check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"pipe96 act{act}")
@@ -272,8 +286,8 @@ def test_pipe_long_runs_c96():
 @pytest.mark.parametrize("nskip", [1, 2])
 @pytest.mark.parametrize("h,w", [(8, 17), (17, 33), (33, 17), (1082, 64), (54, 1920)])
 def test_pipe_residual_c96(nskip, h, w):
-    """96 channels with residual inputs: the producers stage the residual tile
-    in LDS a step ahead (two inputs pre-added in fp16)."""
+    """96 channels with residual inputs: the producers load the residual chunks
+    into registers a step ahead and add them, in graph order, as they store."""
     x, wt, b = make_case(35, 1, 96, 96, h, w)
     rng = np.random.default_rng(36)
     skips = [rng.standard_normal((1, 96, h, w)).astype(np.float16) for _ in range(nskip)]
