@@ -281,3 +281,34 @@ def test_head_reads_boundary_input(io32):
     floor2 = run_model(m, x, round_fp16=False)
     s2, f2 = _compare(got2.astype(np.float32), want2), _compare(floor2, want2)
     assert s2["rel_rms"] <= max(4 * f2["rel_rms"], 2e-3), (s2, f2)
+
+
+@pytest.mark.parametrize("builder", [models.r8f64, models.shipped_like, models.r16f96],
+                         ids=["r8f64", "shipped_like", "r16f96"])
+def test_full_frame_equals_cropped_runs(builder):
+    """Size-independent parity at 1920x1080: every output pixel is a function of
+    its receptive field only (one pixel per 3x3 conv), computed by the same
+    instructions wherever it sits as long as the 2x2 Winograd tile alignment is
+    kept (even offsets). So the full frame, cropped to a window with a margin of
+    at least one pixel per conv, equals a run on that window bit for bit over
+    the window's interior. Windows: the top-left and bottom-right corners (real
+    image edges) and one in the middle. Small runs are pinned to the oracle by
+    test_deep_models_within_fp16_floor; this carries that to full size."""
+    spec = builder(seed=0)
+    n_conv = len(spec.convs)
+    m = n_conv + (n_conv & 1)  # margin, even
+    H, W = 1080, 1920
+    x = models.synthetic_input((1, 1, H, W), seed=7)
+    s = spec.scale
+    with Engine(0) as e:
+        e.build(spec)
+        full = e.run(x)
+        for r0, r1, c0, c1 in ((0, 48, 0, 64), (520, 552, 928, 1000), (H - 40, H, W - 64, W)):
+            a0, a1 = max(r0 - m, 0), min(r1 + m, H)
+            b0, b1 = max(c0 - m, 0), min(c1 + m, W)
+            assert a0 % 2 == 0 and b0 % 2 == 0
+            win = e.run(np.ascontiguousarray(x[:, :, a0:a1, b0:b1]))
+            got = win[:, :, (r0 - a0) * s:(r1 - a0) * s, (c0 - b0) * s:(c1 - b0) * s]
+            want = full[:, :, r0 * s:r1 * s, c0 * s:c1 * s]
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16),
+                                          err_msg=f"{spec.name} window {r0}:{r1},{c0}:{c1}")
