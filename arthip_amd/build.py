@@ -14,9 +14,10 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
+def build(jobs: int | None = None, verbose: bool = False, force: bool = False) -> Path:
+    """force: recompile every source even when the library is up to date."""
     jobs = jobs or min(8, os.cpu_count() or 4)
-    cmd = ["make", "-C", str(CSRC), f"-j{jobs}"]
+    cmd = ["make", "-C", str(CSRC), f"-j{jobs}"] + (["-B"] if force else [])
     if not verbose:
         cmd.append("-s")
     subprocess.run(cmd, check=True)

@@ -18,9 +18,9 @@ LIB_PATH = ORACLE_DIR / "_build" / "liboracle.so"
 _lib = None
 
 
-def build() -> Path:
-    """Compile oracle.c with gcc (oracle/Makefile)."""
-    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+def build(force: bool = False) -> Path:
+    """Compile oracle.c with gcc (oracle/Makefile); force: even when up to date."""
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)] + (["-B"] if force else []), check=True)
     return LIB_PATH
 
 
