@@ -248,3 +248,81 @@ def test_converted_model_builds_like_the_conversion_option():
     a = vs.Model("YUV444PS", 32, 32, SHIPPED["chroma"], fp16=1)
     b = vs.Model("YUV444PS", 32, 32, conv, fp16=0)
     assert (a.in_fp32, a.out_fp32, a.format) == (b.in_fp32, b.out_fp32, b.format)
+
+
+# ---------------------------------------------------------------------------
+# Frame-time refusals (validated before any device work)
+# ---------------------------------------------------------------------------
+
+def _frame_call(m, planes, fmt=None, n_dst=None, null_dst=False, out_stride=None):
+    """Calls arthip_vs_model_get_frame directly with hand-made arguments."""
+    lib = _lib.lib()
+    fmt = m.clip_format if fmt is None else vs.FORMATS[fmt]
+    n = len(planes)
+    pw = (ctypes.c_int * n)(*[p.shape[1] for p in planes])
+    ph = (ctypes.c_int * n)(*[p.shape[0] for p in planes])
+    sp = (ctypes.c_void_p * n)(*[p.ctypes.data for p in planes])
+    ss = (ctypes.c_ssize_t * n)(*[p.strides[0] for p in planes])
+    k = m.planes_written if n_dst is None else n_dst
+    out = np.zeros((planes[0].shape[0] * m.scale_h, planes[0].shape[1] * m.scale_w),
+                   m.format.dtype)
+    dp = (ctypes.c_void_p * max(k, 1))(*([None if null_dst else out.ctypes.data] * k))
+    stride = out.strides[0] if out_stride is None else out_stride
+    ds = (ctypes.c_ssize_t * max(k, 1))(*([stride] * k))
+    err = ctypes.create_string_buffer(512)
+    rc = lib.arthip_vs_model_get_frame(m._h, ctypes.byref(fmt._c()), pw, ph, sp, ss, dp, ds, k,
+                                       err, len(err))
+    return rc, err.value.decode()
+
+
+def test_frame_refusals_before_device_work():
+    with make("GRAYH", "luma", width=32, height=32) as m:
+        x = np.zeros((32, 32), np.float16)
+        rc, msg = _frame_call(m, [x, x, x], fmt="YUV444PH")
+        assert rc == 2 and "plane count does not match" in msg
+        rc, msg = _frame_call(m, [x], n_dst=0)
+        assert rc == 2 and "destination plane" in msg
+        rc, msg = _frame_call(m, [x], null_dst=True)
+        assert rc == 2 and "null destination" in msg
+        short = np.zeros((32, 8), np.float16)
+        lib = _lib.lib()
+        # A source stride shorter than a row.
+        pw = (ctypes.c_int * 1)(32)
+        ph = (ctypes.c_int * 1)(32)
+        sp = (ctypes.c_void_p * 1)(short.ctypes.data)
+        ss = (ctypes.c_ssize_t * 1)(16)
+        out = np.zeros((64, 64), np.float16)
+        dp = (ctypes.c_void_p * 1)(out.ctypes.data)
+        ds = (ctypes.c_ssize_t * 1)(out.strides[0])
+        err = ctypes.create_string_buffer(512)
+        rc = lib.arthip_vs_model_get_frame(m._h, ctypes.byref(vs.FORMATS["GRAYH"]._c()), pw, ph,
+                                           sp, ss, dp, ds, 1, err, len(err))
+        assert rc == 2 and "stride shorter than a row" in err.value.decode()
+    with make("YUV444PS", "chroma", width=32, height=32) as m:
+        a = np.zeros((32, 32), np.float32)
+        b = np.zeros((16, 16), np.float32)
+        rc, msg = _frame_call(m, [a, b, b])
+        assert rc == 2 and "subsampled input frame" in msg
+        gray10 = vs.VideoFormat("YUV444P10", vs.YUV, vs.INTEGER, 10)
+        lib = _lib.lib()
+        pw = (ctypes.c_int * 3)(32, 32, 32)
+        ph = (ctypes.c_int * 3)(32, 32, 32)
+        sp = (ctypes.c_void_p * 3)(a.ctypes.data, a.ctypes.data, a.ctypes.data)
+        ss = (ctypes.c_ssize_t * 3)(128, 128, 128)
+        out = np.zeros((32, 32), np.float32)
+        dp = (ctypes.c_void_p * 1)(out.ctypes.data)
+        ds = (ctypes.c_ssize_t * 1)(128)
+        err = ctypes.create_string_buffer(512)
+        rc = lib.arthip_vs_model_get_frame(m._h, ctypes.byref(gray10._c()), pw, ph, sp, ss, dp,
+                                           ds, 1, err, len(err))
+        assert rc == 2 and "8/16-bit int or fp16/fp32" in err.value.decode()
+
+
+def test_null_arguments_are_refused():
+    lib = _lib.lib()
+    err = ctypes.create_string_buffer(256)
+    out = ctypes.c_void_p()
+    rc = lib.arthip_vs_model_create(None, 1, None, 64, 64, ctypes.byref(out), None, err, 256)
+    assert rc == 1 and "null argument" in err.value.decode() and not out.value
+    rc = lib.arthip_vs_model_get_frame(None, None, None, None, None, None, None, None, 0, err, 256)
+    assert rc == 2 and "null model" in err.value.decode()
