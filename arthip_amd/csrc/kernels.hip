@@ -2477,7 +2477,10 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
                                                        0) != hipSuccess ||
           occ < 1)
         occ = 1;
-      int64_t grid = (int64_t)cu_count() * occ;  // every workgroup resident
+      // Two workgroups per CU at most: longer column walks amortise each
+      // workgroup's six-row prologue (1080p 1 -> 64: 68 us with four per CU,
+      // 64 us with two, 72 us with one).
+      int64_t grid = (int64_t)cu_count() * (occ > 2 ? 2 : occ);
       if (grid > items) grid = items;
       grid = (grid + 7) / 8 * 8;
       hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), 0, s, a, n_seg, (int)items, fs, fh);
