@@ -290,9 +290,14 @@ int arthip_ep_get_capability(const void* model, size_t size, int device_id, int*
     return report("null model or output count", ARTHIP_ERR_BUILD, err, errlen);
   if (device_id >= 0) {
     // Context initialization (hip_execution_provider.cc:163-176): a device that
-    // cannot be selected and initialized gets no nodes.
-    if (hipSetDevice(device_id) != hipSuccess || hipFree(nullptr) != hipSuccess) {
-      (void)hipGetLastError();
+    // cannot be selected and initialized gets no nodes. The calling thread's
+    // current device is restored afterwards.
+    int prev = -1;
+    const bool had = hipGetDevice(&prev) == hipSuccess;
+    const bool ok = hipSetDevice(device_id) == hipSuccess && hipFree(nullptr) == hipSuccess;
+    if (had) (void)hipSetDevice(prev);
+    (void)hipGetLastError();
+    if (!ok) {
       copy_out("", err, errlen);
       return ARTHIP_OK;
     }
