@@ -324,6 +324,43 @@ int arthip_ep_get_capability(const void* model, size_t size, int device_id, int*
   return ARTHIP_OK;
 }
 
+// Writes names NUL-separated into (buf, len); false when they do not fit.
+static bool pack_names(const std::vector<std::string>& names, char* buf, int len) {
+  size_t need = 0;
+  for (const auto& n : names) need += n.size() + 1;
+  if (need > 0 && (buf == nullptr || need > static_cast<size_t>(len < 0 ? 0 : len))) return false;
+  size_t k = 0;
+  for (const auto& n : names) {
+    std::memcpy(buf + k, n.data(), n.size());
+    k += n.size();
+    buf[k++] = '\0';
+  }
+  return true;
+}
+
+int arthip_ep_run_boundary(const void* model, size_t size, const int* nodes, int n_nodes,
+                           char* activations, int activations_len, int* n_activations,
+                           char* constants, int constants_len, int* n_constants, char* outputs,
+                           int outputs_len, int* n_outputs, char* err, int errlen) {
+  if (model == nullptr || (n_nodes > 0 && nodes == nullptr))
+    return report("null model or node list", ARTHIP_ERR_BUILD, err, errlen);
+  arthip::onnx::Model m;
+  std::string e;
+  if (!arthip::onnx::ParseModel(model, size, m, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  std::vector<std::string> acts, consts, outs;
+  const std::vector<int> run(nodes, nodes + (n_nodes > 0 ? n_nodes : 0));
+  if (!arthip::EpRunBoundary(m, run, acts, consts, outs, e))
+    return report(e, ARTHIP_ERR_BUILD, err, errlen);
+  if (n_activations) *n_activations = static_cast<int>(acts.size());
+  if (n_constants) *n_constants = static_cast<int>(consts.size());
+  if (n_outputs) *n_outputs = static_cast<int>(outs.size());
+  if (!pack_names(acts, activations, activations_len) ||
+      !pack_names(consts, constants, constants_len) || !pack_names(outs, outputs, outputs_len))
+    return report("name buffers are too small", ARTHIP_ERR_BUILD, err, errlen);
+  copy_out("", err, errlen);
+  return ARTHIP_OK;
+}
+
 int arthip_engine_build_subgraph(arthip_engine* eng, const void* model, size_t size,
                                  const int* nodes, int n_nodes, char* err, int errlen) {
   if (eng == nullptr || model == nullptr || (n_nodes > 0 && nodes == nullptr))

@@ -219,9 +219,13 @@ bool EpPartition(const onnx::Model& m, std::vector<EpRun>& runs, std::string& er
   return true;
 }
 
-bool EpRunModel(const onnx::Model& m, const std::vector<int>& run, onnx::Model& out,
-                std::string& error) {
+bool EpRunBoundary(const onnx::Model& m, const std::vector<int>& run,
+                   std::vector<std::string>& acts, std::vector<std::string>& consts,
+                   std::vector<std::string>& outs, std::string& error) {
   const auto& nodes = m.graph.nodes;
+  acts.clear();
+  consts.clear();
+  outs.clear();
   if (run.empty()) {
     error = "empty node run";
     return false;
@@ -238,8 +242,16 @@ bool EpRunModel(const onnx::Model& m, const std::vector<int>& run, onnx::Model& 
   for (const auto& n : nodes)
     for (const auto& x : n.inputs)
       if (!x.empty()) ++total_consumers[x];
-  std::vector<std::string> acts, consts, outs;
   run_boundary(m, inits, total_consumers, graph_outputs, run, acts, consts, outs);
+  return true;
+}
+
+bool EpRunModel(const onnx::Model& m, const std::vector<int>& run, onnx::Model& out,
+                std::string& error) {
+  const auto& nodes = m.graph.nodes;
+  const Inits inits = initializers(m);
+  std::vector<std::string> acts, consts, outs;
+  if (!EpRunBoundary(m, run, acts, consts, outs, error)) return false;
   if (acts.size() != 1 || outs.size() != 1) {
     error = "a run needs exactly one activation input and one output (has " +
             std::to_string(acts.size()) + " and " + std::to_string(outs.size()) + ")";

@@ -40,6 +40,13 @@ bool EpNodeSupported(const onnx::Model& model, const TypeMap& types, int i);
 // or more than one needed output are not claimed.
 bool EpPartition(const onnx::Model& model, std::vector<EpRun>& runs, std::string& error);
 
+// The boundary of a node run (any run, claimed or not): its external
+// activations, the initializers it reads and the outputs needed outside it,
+// each deduplicated in first-seen order (hip_execution_provider.cc:244-297).
+bool EpRunBoundary(const onnx::Model& model, const std::vector<int>& nodes,
+                   std::vector<std::string>& activations, std::vector<std::string>& constants,
+                   std::vector<std::string>& outputs, std::string& error);
+
 // The model of one run: its nodes, the initializers they read, and the run's
 // input and output as graph input and output with their inferred types.
 bool EpRunModel(const onnx::Model& model, const std::vector<int>& nodes, onnx::Model& out,

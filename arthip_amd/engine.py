@@ -64,6 +64,27 @@ def get_capability(model, device_id: int = -1) -> list[list[int]]:
     raise EngineError(_msg(e, "get_capability failed"))
 
 
+def run_boundary(model, nodes) -> tuple[list[str], list[str], list[str]]:
+    """The fused node's MetaDef for a node run: (activations, constants, outputs)."""
+    lib = _lib.lib()
+    data = model_bytes(model)
+    buf = ctypes.create_string_buffer(data, len(data))
+    idx = (ctypes.c_int * max(len(nodes), 1))(*nodes)
+    size = 1 << 16
+    bufs = [ctypes.create_string_buffer(size) for _ in range(3)]
+    counts = [ctypes.c_int() for _ in range(3)]
+    e = _err()
+    rc = lib.arthip_ep_run_boundary(buf, len(data), idx, len(nodes), bufs[0], size,
+                                    ctypes.byref(counts[0]), bufs[1], size, ctypes.byref(counts[1]),
+                                    bufs[2], size, ctypes.byref(counts[2]), e, _ERR_LEN)
+    if rc != 0:
+        raise EngineError(_msg(e, f"run_boundary failed (rc={rc})"))
+
+    def names(b, n):
+        return b.raw.split(b"\0")[:n.value] if n.value else []
+    return tuple([x.decode() for x in names(b, n)] for b, n in zip(bufs, counts))
+
+
 def _err() -> ctypes.Array:
     return ctypes.create_string_buffer(_ERR_LEN)
 

@@ -104,6 +104,17 @@ int arthip_ep_get_capability(const void* model, size_t size, int device_id, int*
                              int* run_start, int max_runs, int* n_nodes, int* nodes,
                              int max_nodes, char* err, int errlen);
 
+/* The fused node's MetaDef for a run (hip_execution_provider.cc:244-330): its
+ * external activations (the claimed runs have exactly one, input 0), the
+ * initializers its nodes read (the inputs after it) and the outputs needed
+ * outside it, each deduplicated in first-seen order. Names are written
+ * NUL-separated into the three buffers, with their counts; returns 1 when the
+ * node list is invalid or a buffer is too small. */
+int arthip_ep_run_boundary(const void* model, size_t size, const int* nodes, int n_nodes,
+                           char* activations, int activations_len, int* n_activations,
+                           char* constants, int constants_len, int* n_constants, char* outputs,
+                           int outputs_len, int* n_outputs, char* err, int errlen);
+
 /* Compile for one claimed run (hip_execution_provider.cc:337-357): builds the
  * engine from the run's nodes of the serialized model, with the run's single
  * activation as input 0 and its single output as output 0. */

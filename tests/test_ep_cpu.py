@@ -201,3 +201,27 @@ def test_boundary_casts_only():
     m2 = _model(mid, "x", [1, 1, "h", "w"], F32, "y", [1, 1, "h", "w"], F32,
                 [_half("w", w), _half("w2", w2)])
     assert claims(m2) == [[0, 1], [4, 5]]
+
+
+# ---------------------------------------------------------------------------
+# The fused node's MetaDef (activation input, initializers, outputs)
+# ---------------------------------------------------------------------------
+
+def test_run_boundary(fixtures):
+    from arthip_amd.engine import run_boundary
+    m = fixtures.get("ep_two_convs_one_input").model
+    acts, consts, outs = run_boundary(m, [0, 1, 2])
+    assert acts == ["x"] and outs == ["y"]
+    assert consts == ["w1", "b1", "w2", "b2"]
+    # A sub-run exports what the rest of the graph reads.
+    acts, consts, outs = run_boundary(m, [0, 1])
+    assert acts == ["x"] and consts == ["w1", "b1", "w2", "b2"] and outs == ["ca", "cb"]
+    g = op.Graph(nodes=[op.node("Add", ["x1", "x2"], ["y"])],
+                 inputs=[op.value_info("x1", F16, [1, 4, "h", "w"]),
+                         op.value_info("x2", F16, [1, 4, "h", "w"])],
+                 outputs=[op.value_info("y", F16, [1, 4, "h", "w"])])
+    assert run_boundary(op.Model(graph=g), [0]) == (["x1", "x2"], [], ["y"])
+    with pytest.raises(EngineError, match="increasing"):
+        run_boundary(m, [1, 0])
+    with pytest.raises(EngineError, match="empty"):
+        run_boundary(m, [])
