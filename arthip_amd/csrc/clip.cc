@@ -1,6 +1,7 @@
 #include "clip.h"
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "launch.h"
@@ -99,9 +100,14 @@ struct ClipModel::Slot {
   void* out_host = nullptr;
   size_t raw_host_cap = 0, raw_dev_cap = 0, in_cap = 0, out_cap = 0, out_int_cap = 0,
          out_host_cap = 0;
+  // Profiling: events after the engine's last launch and after the download.
+  hipEvent_t ev_run = nullptr, ev_dl = nullptr;
+  uint64_t frames = 0;
 
   ~Slot() {
     if (stream) hipStreamSynchronize(stream);
+    if (ev_run) hipEventDestroy(ev_run);
+    if (ev_dl) hipEventDestroy(ev_dl);
     if (raw_host) hipHostFree(raw_host);
     if (out_host) hipHostFree(out_host);
     for (void* p : {raw_dev, in_dev, out_dev, out_int_dev})
@@ -172,6 +178,10 @@ std::unique_ptr<ClipModel> ClipModel::Create(const ClipModelArgs& args, int num_
     return static_cast<int>(v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : v));
   };
   d->device_ = args.has_device_id ? sat(args.device_id) : 0;
+  {
+    const char* e = std::getenv("VSHIP_PROFILE");
+    d->profile_ = e != nullptr && e[0] == '1';
+  }
   int num_streams = args.has_num_streams ? sat(args.num_streams) : 0;
   if (num_streams < 1) num_streams = 1;
   d->fp16_ = args.has_fp16 ? (args.fp16 != 0) : true;
@@ -206,6 +216,7 @@ std::unique_ptr<ClipModel> ClipModel::Create(const ClipModelArgs& args, int num_
     s->eng = std::make_unique<Engine>(d->device_);
     std::string berr;
     if (!s->eng->Build(bytes.data(), bytes.size(), berr, opts)) return fail(berr);
+    if (d->profile_) s->eng->SetProfiling(true);
     d->slots_.push_back(std::move(s));
   }
   Engine& e0 = *d->slots_[0]->eng;
@@ -375,6 +386,11 @@ bool ClipModel::RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h,
   }
   std::string rerr;
   if (!eng.RunDevice(s.in_dev, in_shape, s.out_dev, s.stream, rerr)) return fail(rerr);
+  const bool prof = profile_ && ((s.ev_run != nullptr) ||
+                                 (hipEventCreate(&s.ev_run) == hipSuccess &&
+                                  hipEventCreate(&s.ev_dl) == hipSuccess));
+  if (prof && (e = hipEventRecord(s.ev_run, s.stream)) != hipSuccess)
+    return hip_fail("HIP event record", e);
   const void* dl_src = s.out_dev;
   if (int_out) {
     PlaneArgs pa{s.out_dev, s.out_int_dev, static_cast<int64_t>(out_px * n_out), kSampleF16, kSampleU16};
@@ -383,7 +399,25 @@ bool ClipModel::RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h,
   }
   if ((e = hipMemcpyAsync(s.out_host, dl_src, dl_bytes, hipMemcpyDeviceToHost, s.stream)) != hipSuccess)
     return hip_fail("HIP output download", e);
+  if (prof && (e = hipEventRecord(s.ev_dl, s.stream)) != hipSuccess)
+    return hip_fail("HIP event record", e);
   if ((e = hipStreamSynchronize(s.stream)) != hipSuccess) return hip_fail("HIP stream synchronize", e);
+  if (prof) {
+    std::vector<Engine::StepProfile> steps;
+    std::string perr;
+    if (!eng.ProfileRead(steps, perr)) return fail(perr);
+    const uint64_t f = ++s.frames;
+    if (f <= 3 || f % 128 == 0) {
+      float xfer = 0.0f;
+      hipEventElapsedTime(&xfer, s.ev_run, s.ev_dl);
+      std::fprintf(stderr, "[vship-prof] frame %llu\n", static_cast<unsigned long long>(f));
+      for (size_t i = 0; i < steps.size(); ++i)
+        std::fprintf(stderr, "[vship-prof] op%-2zu %s %8.3f ms\n", i, steps[i].name.c_str(),
+                     steps[i].total_ms);
+      std::fprintf(stderr, "[vship-prof] output-convert+download %8.3f ms\n", xfer);
+      std::fflush(stderr);
+    }
+  }
 
   // Host: rows out of pinned staging into the destination planes.
   const uint8_t* ost = static_cast<const uint8_t*>(s.out_host);

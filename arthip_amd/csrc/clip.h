@@ -100,6 +100,10 @@ class ClipModel {
 
   std::vector<std::unique_ptr<Slot>> slots_;
   std::atomic<unsigned> next_{0};
+  // VSHIP_PROFILE=1 at creation: per-launch GPU spans and the output
+  // conversion + download span on stderr for the first three frames of each
+  // engine and every 128th (hip_engine.cc:1409-1604).
+  bool profile_ = false;
   int device_ = 0;
   bool fp16_ = true;
   bool in_fp32_ = false, out_fp32_ = false;

@@ -12,7 +12,8 @@ in for ONNX Runtime's CPU EP, which is not installed. On top:
 - the load-time fp16 conversion bit for bit against an engine built from the
   oracle's converted model;
 - the engine pool: frames from several threads equal the one-stream results,
-  and a variable-size clip.
+  and a variable-size clip;
+- VSHIP_PROFILE=1 spans (P2-18, 483-512).
 """
 
 from __future__ import annotations
@@ -244,3 +245,21 @@ def test_frame_time_refusals():
         b = np.zeros((16, 16), np.float32)
         with pytest.raises(vs.ModelError, match="subsampled input frame"):
             m.get_frame([a, b, b])
+
+
+def test_profiling_reports_ops_and_a_separate_transfer(capfd, monkeypatch):
+    """VSHIP_PROFILE=1 (test_plugin.py P2-18): per-op GPU spans and the output
+    conversion + download as its own span, not folded into the last op."""
+    monkeypatch.setenv("VSHIP_PROFILE", "1")
+    x = np.random.default_rng(13).uniform(0, 1, (48, 64)).astype(np.float16)
+    with vs.Model("GRAYH", 64, 48, LUMA, fp16=0) as m:  # GRAY16 out: a conversion kernel too
+        for _ in range(2):
+            m.get_frame([x])
+    err = capfd.readouterr().err
+    assert "[vship-prof]" in err, err
+    assert "output-convert+download" in err, err
+    ops = [ln for ln in err.splitlines() if ln.startswith("[vship-prof] op")]
+    assert len(ops) >= 2 * 27, err  # both frames, every launch of the shipped model
+    for ln in ops:
+        ms = float(ln.split()[-2])
+        assert 0.0 <= ms < 1000.0, ln
