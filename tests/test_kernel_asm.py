@@ -1,0 +1,110 @@
+"""LDS ordering at every workgroup barrier, checked without a GPU.
+
+Mirrors the reference's kernel memory-ordering gate (tests/correctness/
+test_kernel.py): an `s_barrier` orders control flow but does not retire
+outstanding LDS stores, so a wave could pass a barrier with its stores still in
+flight and another wave read stale shared memory (the corruption the reference's
+NOTES.md describes). Every barrier in kernels.hip goes through `lds_sync`, which
+emits `s_waitcnt lgkmcnt(0)` itself instead of relying on the compiler's waitcnt
+pass. Checked two ways:
+- in the source: `__syncthreads` appears only inside `lds_sync`;
+- in the gfx950 assembly hipcc emits for kernels.hip: in every kernel, walking
+  back from each `s_barrier` inside its basic block, an `s_waitcnt lgkmcnt(0)`
+  comes before any LDS instruction (the compiler may schedule ALU work between
+  the drain and the barrier, which is harmless).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+CSRC = Path(__file__).resolve().parents[1] / "arthip_amd" / "csrc"
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+
+def _strip_comments(text: str) -> str:
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.sub(r"//[^\n]*", "", text)
+
+
+def test_barriers_only_through_lds_sync():
+    src = _strip_comments((CSRC / "kernels.hip").read_text())
+    m = re.search(r"void lds_sync\(\)\s*\{(.*?)\n\}", src, flags=re.S)
+    assert m, "lds_sync not found"
+    body = m.group(1)
+    assert "lgkmcnt(0)" in body and "__syncthreads" in body
+    rest = src[:m.start()] + src[m.end():]
+    assert "__syncthreads" not in rest, "a barrier outside lds_sync"
+    assert "s_barrier" not in rest, "a raw s_barrier outside lds_sync"
+
+
+@pytest.fixture(scope="session")
+def kernel_asm(tmp_path_factory) -> str:
+    if not Path(HIPCC).exists():
+        pytest.skip("hipcc not available")
+    src = CSRC / "kernels.hip"
+    digest = hashlib.sha1(src.read_bytes()).hexdigest()[:12]
+    out = tmp_path_factory.mktemp("asm") / f"kernels_{digest}.s"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S", "-o", str(out), str(src)]
+    subprocess.run(cmd, check=True, cwd=CSRC, capture_output=True)
+    return out.read_text()
+
+
+def _kernels(asm: str):
+    """(symbol, instruction list) for every kernel in the assembly."""
+    lines = asm.splitlines()
+    i = 0
+    while i < len(lines):
+        m = re.match(r"^(_Z\S+):\s*(;.*)?$", lines[i])
+        if m and ".amdhsa" not in lines[i]:
+            name = m.group(1)
+            body = []
+            i += 1
+            while i < len(lines) and not lines[i].startswith(".Lfunc_end"):
+                t = lines[i].split(";", 1)[0].strip()
+                if t.endswith(":"):
+                    body.append(":label")  # a basic block starts: other paths join here
+                elif t and not t.startswith("."):
+                    body.append(t)
+                i += 1
+            yield name, body
+        i += 1
+
+
+def _drained(ins, k) -> bool:
+    """Walking back from instruction k in its basic block: a drain before any
+    LDS instruction (ds_*) or the block's start."""
+    for t in reversed(ins[:k]):
+        if t.startswith("s_waitcnt") and "lgkmcnt(0)" in t:
+            return True
+        if t.startswith("ds_") or t == ":label":
+            return False
+    return False
+
+
+def test_every_barrier_is_preceded_by_an_lds_drain(kernel_asm):
+    checked = 0
+    for name, ins in _kernels(kernel_asm):
+        for k, t in enumerate(ins):
+            if t.startswith("s_barrier"):
+                assert _drained(ins, k), (
+                    f"{name}: barrier at instruction {k} is reached with LDS work not drained: "
+                    f"{ins[max(0, k - 8):k]}")
+                checked += 1
+    assert checked > 100, f"only {checked} barriers found; the assembly parse looks wrong"
+
+
+def test_drain_check_catches_a_missing_drain():
+    """The checker itself: a store, then a barrier, fails; a drain in between,
+    or only ALU work after the drain, passes."""
+    assert not _drained(["ds_write_b128 v1, v[2:5]", "s_barrier"], 1)
+    assert _drained(["ds_write_b128 v1, v[2:5]", "s_waitcnt lgkmcnt(0)", "v_add_u32 v1, v2, v3",
+                     "s_barrier"], 3)
+    assert not _drained([":label", "v_add_u32 v1, v2, v3", "s_barrier"], 2)
