@@ -85,13 +85,45 @@ bool load_network(const ClipModelArgs& args, std::vector<uint8_t>& bytes, std::s
 
 }  // namespace
 
-// One engine of the pool with its stream and the staging of one frame shape.
-struct ClipModel::Slot {
-  std::unique_ptr<Engine> eng;
-  std::mutex mu;
-  hipStream_t stream = nullptr;
-  // Raw plane samples (host pinned + device), the engine's boundary input and
-  // output, and the integer output.
+namespace {
+
+bool grow_dev(void*& p, size_t& cap, size_t need, std::string& error) {
+  if (need <= cap) return true;
+  if (p) hipFree(p);
+  p = nullptr;
+  cap = 0;
+  const hipError_t e = hipMalloc(&p, need);
+  if (e != hipSuccess) {
+    p = nullptr;
+    error = std::string("hipMalloc failed: ") + hipGetErrorString(e);
+    return false;
+  }
+  cap = need;
+  return true;
+}
+
+bool grow_host(void*& p, size_t& cap, size_t need, std::string& error) {
+  if (need <= cap) return true;
+  if (p) hipHostFree(p);
+  p = nullptr;
+  cap = 0;
+  const hipError_t e = hipHostMalloc(&p, need, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    p = nullptr;
+    error = std::string("hipHostMalloc failed: ") + hipGetErrorString(e);
+    return false;
+  }
+  cap = need;
+  return true;
+}
+
+}  // namespace
+
+// The staging of one frame in flight: raw plane samples (pinned host +
+// device), the engine's boundary input and output, the integer output, the
+// pinned download, and the event that marks the download done.
+struct ClipModel::Io {
+  std::mutex mu;  // held for a whole frame
   void* raw_host = nullptr;
   void* raw_dev = nullptr;
   void* in_dev = nullptr;
@@ -100,48 +132,58 @@ struct ClipModel::Slot {
   void* out_host = nullptr;
   size_t raw_host_cap = 0, raw_dev_cap = 0, in_cap = 0, out_cap = 0, out_int_cap = 0,
          out_host_cap = 0;
-  // Profiling: events after the engine's last launch and after the download.
-  hipEvent_t ev_run = nullptr, ev_dl = nullptr;
-  uint64_t frames = 0;
+  // Upload landed / kernels done / download done.
+  hipEvent_t up = nullptr, comp = nullptr, done = nullptr;
 
-  ~Slot() {
-    if (stream) hipStreamSynchronize(stream);
-    if (ev_run) hipEventDestroy(ev_run);
-    if (ev_dl) hipEventDestroy(ev_dl);
+  ~Io() {
+    if (done) hipEventSynchronize(done);
+    for (hipEvent_t ev : {up, comp, done})
+      if (ev) hipEventDestroy(ev);
     if (raw_host) hipHostFree(raw_host);
     if (out_host) hipHostFree(out_host);
     for (void* p : {raw_dev, in_dev, out_dev, out_int_dev})
       if (p) hipFree(p);
-    if (stream) hipStreamDestroy(stream);
   }
+};
 
-  static bool grow_dev(void*& p, size_t& cap, size_t need, std::string& error) {
-    if (need <= cap) return true;
-    if (p) hipFree(p);
-    p = nullptr;
-    cap = 0;
-    const hipError_t e = hipMalloc(&p, need);
-    if (e != hipSuccess) {
-      p = nullptr;
-      error = std::string("hipMalloc failed: ") + hipGetErrorString(e);
-      return false;
-    }
-    cap = need;
-    return true;
+// Upload and download streams shared by every engine of the pool: PCIe is one
+// resource, and one kernel stream per engine plus these two stays within the
+// process's hardware queues (more streams than queues share queues and
+// serialize).
+struct ClipModel::CopyStreams {
+  std::mutex mu;  // creation
+  hipStream_t up = nullptr, down = nullptr;  // host -> device, device -> host
+
+  ~CopyStreams() {
+    for (hipStream_t st : {up, down})
+      if (st) hipStreamSynchronize(st);
+    for (hipStream_t st : {up, down})
+      if (st) hipStreamDestroy(st);
   }
-  static bool grow_host(void*& p, size_t& cap, size_t need, std::string& error) {
-    if (need <= cap) return true;
-    if (p) hipHostFree(p);
-    p = nullptr;
-    cap = 0;
-    const hipError_t e = hipHostMalloc(&p, need, hipHostMallocDefault);
-    if (e != hipSuccess) {
-      p = nullptr;
-      error = std::string("hipHostMalloc failed: ") + hipGetErrorString(e);
-      return false;
-    }
-    cap = need;
-    return true;
+};
+
+// One engine of the pool with its kernel stream and two staging sets. The
+// engine lock covers only the enqueue of a frame's device work, and uploads and
+// downloads run on the copy streams (ordered against the kernels by events), so
+// one frame's host copies, wait and PCIe transfers overlap the next frame's
+// kernels: with one engine and several callers, the frame time is the kernels'.
+struct ClipModel::Slot {
+  std::unique_ptr<Engine> eng;
+  std::mutex mu;  // engine, stream, last shape; held while enqueuing
+  hipStream_t stream = nullptr;              // kernels
+  hipStream_t up = nullptr, down = nullptr;  // the pool's copy streams (not owned)
+  int64_t last_shape[4] = {0, 0, 0, 0};
+  Io io[2];
+  // Profiling: an event after the engine's last launch (frames then run one at
+  // a time per engine, so each frame's spans are read alone).
+  hipEvent_t ev_run = nullptr;
+  uint64_t frames = 0;
+
+  ~Slot() {
+    for (hipStream_t st : {up, stream, down})
+      if (st) hipStreamSynchronize(st);
+    if (ev_run) hipEventDestroy(ev_run);
+    if (stream) hipStreamDestroy(stream);
   }
 };
 
@@ -211,6 +253,7 @@ std::unique_ptr<ClipModel> ClipModel::Create(const ClipModelArgs& args, int num_
   opts.fp16 = d->fp16_;
   opts.keep_io_fp32 = fmt.sample_type == kStFloat && fmt.bits_per_sample == 32;
 
+  d->copy_ = std::make_unique<CopyStreams>();
   for (int i = 0; i < num_streams; ++i) {
     auto s = std::make_unique<Slot>();
     s->eng = std::make_unique<Engine>(d->device_);
@@ -256,21 +299,24 @@ std::unique_ptr<ClipModel> ClipModel::Create(const ClipModelArgs& args, int num_
   return d;
 }
 
-ClipModel::Slot& ClipModel::Acquire(std::unique_lock<std::mutex>& lock) {
-  // Round-robin start (vs_hip.cpp:121-123), but take the first idle engine
-  // from there instead of queueing behind a busy one.
+ClipModel::Slot& ClipModel::Acquire(std::unique_lock<std::mutex>& lock, Io*& io) {
+  // Round-robin start (vs_hip.cpp:121-123), but take the first idle staging
+  // set from there instead of queueing behind a busy engine.
   const unsigned n = static_cast<unsigned>(slots_.size());
-  const unsigned start = next_.fetch_add(1) % n;
-  for (unsigned k = 0; k < n; ++k) {
+  const unsigned start = next_.fetch_add(1);
+  for (unsigned k = 0; k < 2 * n; ++k) {
     Slot& s = *slots_[(start + k) % n];
-    std::unique_lock<std::mutex> l(s.mu, std::try_to_lock);
+    Io& cand = s.io[((start + k) / n) & 1];
+    std::unique_lock<std::mutex> l(cand.mu, std::try_to_lock);
     if (l.owns_lock()) {
       lock = std::move(l);
+      io = &cand;
       return s;
     }
   }
-  Slot& s = *slots_[start];
-  lock = std::unique_lock<std::mutex>(s.mu);
+  Slot& s = *slots_[start % n];
+  io = &s.io[(start / n) & 1];
+  lock = std::unique_lock<std::mutex>(io->mu);
   return s;
 }
 
@@ -308,11 +354,12 @@ bool ClipModel::GetFrame(const VideoFormat& fmt, const int* plane_w, const int* 
     if (dst[c] == nullptr) return fail("null destination plane");
 
   std::unique_lock<std::mutex> lock;
-  Slot& s = Acquire(lock);
-  return RunSlot(s, fmt, in_c, in_w, in_h, src, src_stride, dst, dst_stride, error);
+  Io* io = nullptr;
+  Slot& s = Acquire(lock, io);
+  return RunSlot(s, *io, fmt, in_c, in_w, in_h, src, src_stride, dst, dst_stride, error);
 }
 
-bool ClipModel::RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h,
+bool ClipModel::RunSlot(Slot& s, Io& io, const VideoFormat& fmt, int in_c, int w, int h,
                         const void* const* src, const ptrdiff_t* src_stride, void* const* dst,
                         const ptrdiff_t* dst_stride, std::string& error) {
   auto fail = [&](const std::string& msg) {
@@ -331,13 +378,6 @@ bool ClipModel::RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h,
   const int out_w = static_cast<int>(out_shape[3]);
   const int n_out = planes_written() < out_c ? planes_written() : out_c;
 
-  hipError_t e = hipSetDevice(device_);
-  if (e != hipSuccess) return hip_fail("hipSetDevice", e);
-  if (s.stream == nullptr && (e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking)) != hipSuccess) {
-    s.stream = nullptr;
-    return hip_fail("hipStreamCreate", e);
-  }
-
   const int src_kind = sample_kind(fmt);
   const int in_kind = in_fp32_ ? kSampleF32 : kSampleF16;
   const size_t in_px = static_cast<size_t>(w) * h;
@@ -355,17 +395,15 @@ bool ClipModel::RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h,
   for (int c = 0; c < n_out; ++c)
     if (dst_stride[c] < static_cast<ptrdiff_t>(orow)) return fail("destination stride shorter than a row");
 
+  hipError_t e = hipSetDevice(device_);
+  if (e != hipSuccess) return hip_fail("hipSetDevice", e);
   std::string aerr;
-  if (!Slot::grow_host(s.raw_host, s.raw_host_cap, raw_bytes, aerr) ||
-      !Slot::grow_dev(s.in_dev, s.in_cap, in_bytes, aerr) ||
-      (!direct_in && !Slot::grow_dev(s.raw_dev, s.raw_dev_cap, raw_bytes, aerr)) ||
-      !Slot::grow_dev(s.out_dev, s.out_cap, out_bytes, aerr) ||
-      (int_out && !Slot::grow_dev(s.out_int_dev, s.out_int_cap, dl_bytes, aerr)) ||
-      !Slot::grow_host(s.out_host, s.out_host_cap, dl_bytes, aerr))
+  if (!grow_host(io.raw_host, io.raw_host_cap, raw_bytes, aerr) ||
+      !grow_host(io.out_host, io.out_host_cap, dl_bytes, aerr))
     return fail(aerr);
 
   // Host: plane rows into pinned staging, plane-major, samples as they are.
-  uint8_t* stage = static_cast<uint8_t*>(s.raw_host);
+  uint8_t* stage = static_cast<uint8_t*>(io.raw_host);
   for (int c = 0; c < in_c; ++c) {
     const uint8_t* base = static_cast<const uint8_t*>(src[c]);
     uint8_t* out = stage + static_cast<size_t>(c) * raw_row * h;
@@ -377,50 +415,105 @@ bool ClipModel::RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h,
                     raw_row);
     }
   }
-  void* upload_dst = direct_in ? s.in_dev : s.raw_dev;
-  if ((e = hipMemcpyAsync(upload_dst, s.raw_host, raw_bytes, hipMemcpyHostToDevice, s.stream)) != hipSuccess)
-    return hip_fail("HIP input upload", e);
-  if (!direct_in) {
-    PlaneArgs pa{s.raw_dev, s.in_dev, static_cast<int64_t>(in_px * in_c), src_kind, in_kind};
-    if ((e = launch_plane_convert(pa, s.stream)) != hipSuccess) return hip_fail("plane_convert", e);
-  }
-  std::string rerr;
-  if (!eng.RunDevice(s.in_dev, in_shape, s.out_dev, s.stream, rerr)) return fail(rerr);
-  const bool prof = profile_ && ((s.ev_run != nullptr) ||
-                                 (hipEventCreate(&s.ev_run) == hipSuccess &&
-                                  hipEventCreate(&s.ev_dl) == hipSuccess));
-  if (prof && (e = hipEventRecord(s.ev_run, s.stream)) != hipSuccess)
-    return hip_fail("HIP event record", e);
-  const void* dl_src = s.out_dev;
-  if (int_out) {
-    PlaneArgs pa{s.out_dev, s.out_int_dev, static_cast<int64_t>(out_px * n_out), kSampleF16, kSampleU16};
-    if ((e = launch_plane_convert(pa, s.stream)) != hipSuccess) return hip_fail("plane_convert", e);
-    dl_src = s.out_int_dev;
-  }
-  if ((e = hipMemcpyAsync(s.out_host, dl_src, dl_bytes, hipMemcpyDeviceToHost, s.stream)) != hipSuccess)
-    return hip_fail("HIP output download", e);
-  if (prof && (e = hipEventRecord(s.ev_dl, s.stream)) != hipSuccess)
-    return hip_fail("HIP event record", e);
-  if ((e = hipStreamSynchronize(s.stream)) != hipSuccess) return hip_fail("HIP stream synchronize", e);
-  if (prof) {
-    std::vector<Engine::StepProfile> steps;
-    std::string perr;
-    if (!eng.ProfileRead(steps, perr)) return fail(perr);
-    const uint64_t f = ++s.frames;
-    if (f <= 3 || f % 128 == 0) {
-      float xfer = 0.0f;
-      hipEventElapsedTime(&xfer, s.ev_run, s.ev_dl);
-      std::fprintf(stderr, "[vship-prof] frame %llu\n", static_cast<unsigned long long>(f));
-      for (size_t i = 0; i < steps.size(); ++i)
-        std::fprintf(stderr, "[vship-prof] op%-2zu %s %8.3f ms\n", i, steps[i].name.c_str(),
-                     steps[i].total_ms);
-      std::fprintf(stderr, "[vship-prof] output-convert+download %8.3f ms\n", xfer);
-      std::fflush(stderr);
+
+  {
+    // Device work of the frame, enqueued under the engine lock. With profiling
+    // the lock covers the whole frame.
+    std::unique_lock<std::mutex> elock(s.mu);
+    // After a failure, work already queued may still read this staging set,
+    // which the next caller may reuse: drain the stream before returning.
+    auto drain = [&](bool r) {
+      if (!r)
+        for (hipStream_t st : {s.up, s.stream, s.down})
+          if (st) (void)hipStreamSynchronize(st);
+      return r;
+    };
+    if (s.up == nullptr) {
+      std::lock_guard<std::mutex> g(copy_->mu);
+      for (hipStream_t* st : {&copy_->up, &copy_->down})
+        if (*st == nullptr && (e = hipStreamCreateWithFlags(st, hipStreamNonBlocking)) != hipSuccess) {
+          *st = nullptr;
+          return hip_fail("hipStreamCreate", e);
+        }
+      s.up = copy_->up;
+      s.down = copy_->down;
+    }
+    if (s.stream == nullptr && (e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking)) != hipSuccess) {
+      s.stream = nullptr;
+      return hip_fail("hipStreamCreate", e);
+    }
+    for (hipEvent_t* ev : {&io.up, &io.comp, &io.done})
+      if (*ev == nullptr && (e = hipEventCreateWithFlags(ev, hipEventDisableTiming)) != hipSuccess) {
+        *ev = nullptr;
+        return hip_fail("hipEventCreate", e);
+      }
+    // A new frame shape re-plans the engine, which frees buffers that earlier
+    // frames may still use: drain first.
+    if (std::memcmp(s.last_shape, in_shape, sizeof in_shape) != 0) {
+      for (hipStream_t st : {s.up, s.stream, s.down})
+        if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail("HIP stream synchronize", e);
+      std::memcpy(s.last_shape, in_shape, sizeof in_shape);
+    }
+    if (!grow_dev(io.in_dev, io.in_cap, in_bytes, aerr) ||
+        (!direct_in && !grow_dev(io.raw_dev, io.raw_dev_cap, raw_bytes, aerr)) ||
+        !grow_dev(io.out_dev, io.out_cap, out_bytes, aerr) ||
+        (int_out && !grow_dev(io.out_int_dev, io.out_int_cap, dl_bytes, aerr)))
+      return fail(aerr);
+    void* upload_dst = direct_in ? io.in_dev : io.raw_dev;
+    if ((e = hipMemcpyAsync(upload_dst, io.raw_host, raw_bytes, hipMemcpyHostToDevice, s.up)) != hipSuccess ||
+        (e = hipEventRecord(io.up, s.up)) != hipSuccess ||
+        (e = hipStreamWaitEvent(s.stream, io.up, 0)) != hipSuccess)
+      return drain(hip_fail("HIP input upload", e));
+    if (!direct_in) {
+      PlaneArgs pa{io.raw_dev, io.in_dev, static_cast<int64_t>(in_px * in_c), src_kind, in_kind};
+      if ((e = launch_plane_convert(pa, s.stream)) != hipSuccess) return drain(hip_fail("plane_convert", e));
+    }
+    std::string rerr;
+    if (!eng.RunDevice(io.in_dev, in_shape, io.out_dev, s.stream, rerr)) return drain(fail(rerr));
+    const bool prof = profile_ && (s.ev_run != nullptr || hipEventCreate(&s.ev_run) == hipSuccess);
+    if (prof && (e = hipEventRecord(s.ev_run, s.stream)) != hipSuccess)
+      return drain(hip_fail("HIP event record", e));
+    const void* dl_src = io.out_dev;
+    if (int_out) {
+      PlaneArgs pa{io.out_dev, io.out_int_dev, static_cast<int64_t>(out_px * n_out), kSampleF16,
+                   kSampleU16};
+      if ((e = launch_plane_convert(pa, s.stream)) != hipSuccess) return drain(hip_fail("plane_convert", e));
+      dl_src = io.out_int_dev;
+    }
+    if ((e = hipEventRecord(io.comp, s.stream)) != hipSuccess ||
+        (e = hipStreamWaitEvent(s.down, io.comp, 0)) != hipSuccess ||
+        (e = hipMemcpyAsync(io.out_host, dl_src, dl_bytes, hipMemcpyDeviceToHost, s.down)) != hipSuccess)
+      return drain(hip_fail("HIP output download", e));
+    if ((e = hipEventRecord(io.done, s.down)) != hipSuccess) return drain(hip_fail("HIP event record", e));
+    if (prof) {
+      if ((e = hipEventSynchronize(io.done)) != hipSuccess) return drain(hip_fail("HIP event synchronize", e));
+      std::vector<Engine::StepProfile> steps;
+      std::string perr;
+      if (!eng.ProfileRead(steps, perr)) return drain(fail(perr));
+      const uint64_t f = ++s.frames;
+      if (f <= 3 || f % 128 == 0) {
+        // io.done has no timing: the transfer span ends at a timed event.
+        hipEvent_t end = nullptr;
+        float xfer = 0.0f;
+        if (hipEventCreate(&end) == hipSuccess) {
+          if (hipEventRecord(end, s.down) == hipSuccess && hipEventSynchronize(end) == hipSuccess)
+            hipEventElapsedTime(&xfer, s.ev_run, end);
+          hipEventDestroy(end);
+        }
+        std::fprintf(stderr, "[vship-prof] frame %llu\n", static_cast<unsigned long long>(f));
+        for (size_t i = 0; i < steps.size(); ++i)
+          std::fprintf(stderr, "[vship-prof] op%-2zu %s %8.3f ms\n", i, steps[i].name.c_str(),
+                       steps[i].total_ms);
+        std::fprintf(stderr, "[vship-prof] output-convert+download %8.3f ms\n", xfer);
+        std::fflush(stderr);
+      }
     }
   }
+  // Outside the engine lock: wait for this frame's download, copy it out.
+  if ((e = hipEventSynchronize(io.done)) != hipSuccess) return hip_fail("HIP output download", e);
 
   // Host: rows out of pinned staging into the destination planes.
-  const uint8_t* ost = static_cast<const uint8_t*>(s.out_host);
+  const uint8_t* ost = static_cast<const uint8_t*>(io.out_host);
   for (int c = 0; c < n_out; ++c) {
     const uint8_t* from = ost + static_cast<size_t>(c) * orow * out_h;
     uint8_t* base = static_cast<uint8_t*>(dst[c]);

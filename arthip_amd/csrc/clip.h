@@ -6,7 +6,8 @@
 // Create validates the clip format and the filter arguments with the
 // reference's rules and error texts (vs_hip.cpp:401-591), loads the model,
 // applies the load-time fp16 conversion and builds num_streams engines.
-// GetFrame runs one frame on a free engine of the pool. Per frame the host only
+// GetFrame runs one frame on an idle staging set of the pool (two per engine:
+// one frame's host copies overlap the next one's device work). Per frame the host only
 // copies plane rows into pinned staging and back out: the samples cross PCIe
 // in their own type (1 byte per 8-bit sample, not a float), and the scaling to
 // [0, 1], the fp16 / fp32 rounding and the integer output conversion run on the
@@ -91,13 +92,18 @@ class ClipModel {
                 const ptrdiff_t* dst_stride, int n_dst, std::string& error);
 
  private:
+  struct Io;
   struct Slot;
+  struct CopyStreams;
   ClipModel() = default;
-  Slot& Acquire(std::unique_lock<std::mutex>& lock);
-  bool RunSlot(Slot& s, const VideoFormat& fmt, int in_c, int w, int h, const void* const* src,
-               const ptrdiff_t* src_stride, void* const* dst, const ptrdiff_t* dst_stride,
-               std::string& error);
+  Slot& Acquire(std::unique_lock<std::mutex>& lock, Io*& io);
+  bool RunSlot(Slot& s, Io& io, const VideoFormat& fmt, int in_c, int w, int h,
+               const void* const* src, const ptrdiff_t* src_stride, void* const* dst,
+               const ptrdiff_t* dst_stride, std::string& error);
 
+  // Declared before slots_ so that the engines' work drains before the shared
+  // copy streams are destroyed.
+  std::unique_ptr<CopyStreams> copy_;
   std::vector<std::unique_ptr<Slot>> slots_;
   std::atomic<unsigned> next_{0};
   // VSHIP_PROFILE=1 at creation: per-launch GPU spans and the output
