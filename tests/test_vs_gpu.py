@@ -222,6 +222,35 @@ def test_pool_threads_match_one_stream():
         np.testing.assert_array_equal(f16_bits(a), f16_bits(b))
 
 
+def test_one_engine_threads_with_changing_frame_sizes():
+    """One engine, two frames in flight, the frame shape changing between them:
+    the engine re-plans only after the other frame's work has drained."""
+    from arthip_amd.engine import Engine
+    rng = np.random.default_rng(13)
+    sizes = [(24, 40), (33, 18), (24, 40), (8, 8), (40, 64), (33, 18)]
+    frames = [rng.uniform(0, 1, sizes[i % len(sizes)]).astype(np.float16) for i in range(24)]
+    with Engine(0) as e:
+        e.build(op.load(LUMA))
+        want = [e.run(f[None, None])[0, 0] for f in frames]
+    got = [None] * len(frames)
+    errors = []
+    with vs.Model("GRAYH", 0, 0, LUMA, num_streams=1) as m:
+        def work(k):
+            try:
+                for i in range(k, len(frames), 4):
+                    got[i] = m.get_frame([frames[i]])[0]
+            except Exception as ex:  # reported below
+                errors.append(ex)
+        threads = [threading.Thread(target=work, args=(k,)) for k in range(4)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+    assert not errors, errors
+    for a, b in zip(got, want):
+        np.testing.assert_array_equal(f16_bits(a), f16_bits(b))
+
+
 def test_variable_size_clip():
     from arthip_amd.engine import Engine
     rng = np.random.default_rng(12)
