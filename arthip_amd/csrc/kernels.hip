@@ -885,10 +885,14 @@ struct PipeL<2> {
 };
 template <>
 struct PipeL<3> {
-  // 208-byte tile rows: the 16 lanes of a B read (16 tiles, one 16-byte
-  // group) land on 16 distinct bank quads. Staging rotates the 12 groups of
+  // 224-byte tile rows (14 of the 16 bank quads). A ds_read_b128 serves 16
+  // lanes per cycle: 8 consecutive lanes of one half of the wave together with
+  // the same 8 of the other half (tiles t..t+7, channel groups g and g+1 for
+  // the B reads), which with 14 quads per row land on 16 distinct quads (14 t
+  // even, +1 odd). 208-byte rows (13 quads) doubled every B read: the counters
+  // read 0.9 conflict cycles per LDS cycle. Staging rotates the 12 groups of
   // pixel x by x >> 1.
-  static constexpr int TS = 104;
+  static constexpr int TS = 112;
   static constexpr int NW = 3;
   __host__ __device__ static constexpr int at(int t, int c) { return t * TS + c; }
   __host__ __device__ static constexpr int st(int row, int x, int g) {
