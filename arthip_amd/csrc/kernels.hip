@@ -1525,6 +1525,11 @@ conv3x3_narrow(NarrowArgs a) {
 // ring filled by global_load_lds the same conv ran at 95 us at 1080p, held
 // back by the DMA issue and LDS bank conflicts.)
 constexpr int TAIL_ROWS = 6;
+// Floats per D tile row: the segment's 64 pixels padded to 18 bank quads, so
+// that the 16 lanes a ds_write_b128 serves per cycle (columns t..t+7 and two
+// adjacent 4-pixel groups) land on 16 distinct quads. Rows of 64 floats put
+// every column on the same quads: 8-way conflicts on each write.
+constexpr int TAIL_TW = 72;
 constexpr int TAIL_SEG = 62;
 
 // Four workgroups per CU for C <= 64 (two for C = 96, whose row window needs
@@ -1538,7 +1543,7 @@ conv3x3_tail(NarrowArgs a) {
   constexpr int PXB = 2 * C;     // bytes per pixel
   constexpr int NR = TAIL_ROWS;  // row slots
   constexpr int SEG = TAIL_SEG;
-  constexpr int TW = 64;         // tile row: the segment's 64 input columns
+  constexpr int TW = TAIL_TW;    // tile row: the segment's 64 input columns, padded
   constexpr int TILE = 16 * TW;  // floats per tile buffer
   extern __shared__ __attribute__((aligned(16))) float nlds[];
   float* const tile = nlds;
@@ -2333,8 +2338,8 @@ hipError_t launch_narrow_kc(const NarrowArgs& a, bool f32, hipStream_t s) {
   const bool rows = narrow_row_packed(a.M);
   NarrowKernel fn = rows ? (f32 ? conv3x3_tail<KC, true> : conv3x3_tail<KC, false>)
                          : (f32 ? conv3x3_narrow<KC, true> : conv3x3_narrow<KC, false>);
-  // conv3x3_tail keeps only its D tiles ([16][64] floats, two buffers) in LDS.
-  const size_t lds = rows ? (size_t)2 * 16 * 64 * 4 : NarrowRing<KC>::lds_bytes();
+  // conv3x3_tail keeps only its D tiles ([16][TAIL_TW] floats, two buffers) in LDS.
+  const size_t lds = rows ? (size_t)2 * 16 * TAIL_TW * 4 : NarrowRing<KC>::lds_bytes();
   if (lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
