@@ -3,6 +3,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 
 #include "launch.h"
 #include "onnx.h"
@@ -428,6 +429,17 @@ bool ClipModel::RunSlot(Slot& s, Io& io, const VideoFormat& fmt, int in_c, int w
           if (st) (void)hipStreamSynchronize(st);
       return r;
     };
+    // The same when the section is left by an exception (an allocation
+    // failure): the caller reports it, and the staging set must be idle first.
+    struct DrainOnThrow {
+      const Slot& s;
+      const int uncaught = std::uncaught_exceptions();
+      ~DrainOnThrow() {
+        if (std::uncaught_exceptions() > uncaught)
+          for (hipStream_t st : {s.up, s.stream, s.down})
+            if (st) (void)hipStreamSynchronize(st);
+      }
+    } drain_on_throw{s};
     if (s.up == nullptr) {
       std::lock_guard<std::mutex> g(copy_->mu);
       for (hipStream_t* st : {&copy_->up, &copy_->down})
