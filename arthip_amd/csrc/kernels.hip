@@ -1977,6 +1977,135 @@ __global__ void __launch_bounds__(256) direct_conv_c1_walk(DirectArgs a, int n_s
   }
 }
 
+// Head conv on MFMA (C = 1, M = 16 * NB with NB even, fast epilogue, no
+// residual inputs). One v_mfma_f32_16x16x16_f16 per 16 pixels and 16 output
+// channels: B holds the 16 pixels' 3 x 3 windows as K = 16 slots (kernel row
+// q in slots 4q .. 4q+2, slot 4q+3 and row 3 zero), so lane (q, j) supplies
+// three input values of pixel j; A holds the taps of 16 output channels in the
+// same slots. The channels of block b are permuted (row i = channel
+// (i / 4) * 4 NB + 4 b + i % 4) so that lane (q, j) ends with the contiguous
+// channels q * 4 NB .. q * 4 NB + 4 NB - 1 of pixel j. Stored from there, each
+// 16-byte store instruction would cover half of every pixel line, and such
+// partial lines with the nontemporal hint cost 154 us instead of 64 at 1080p
+// 1 -> 64. So each wave stages its block (16 pixels, one contiguous stretch of
+// the output row) in its own LDS region and stores it linearly, lane l of
+// instruction s taking 16-byte chunk 64 s + (l ^ 8 for lanes 16-31 and 48-63):
+// whole lines per instruction. LDS operations of one wave complete in order,
+// so the region needs no barrier. Chunk g sits at g ^ ((g >> 3) & 7): the
+// reads are bank-conflict free, the MFMA-layout writes at most 2-way.
+// An item is one output row x 64 pixels (16 per wave); every lane issues the
+// same loads and stores on every path (out-of-range offsets read zero and drop
+// stores), and the next item's loads go out before this item's MFMAs. The
+// products are exact in fp32 and summed in the matrix unit; the epilogue is
+// fast4, as in the other head kernels.
+template <int NB, int ACT, int BIN>
+__global__ void __launch_bounds__(256) direct_conv_c1_mfma(DirectArgs a, int n_seg, int n_items,
+                                                           FastDiv fd_seg, FastDiv fd_H) {
+  static_assert(NB % 2 == 0 && NB <= 6, "16 * NB output channels, NB even");
+  constexpr int M = 16 * NB;
+  constexpr int SEG = 64;
+  constexpr int CH = 2 * NB;    // 16-byte chunks per pixel
+  constexpr int WCH = 16 * CH;  // chunks of a wave's 16-pixel block
+  extern __shared__ __attribute__((aligned(16))) h8 hstage[];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int j = lane & 15;  // pixel of the wave's 16 (B column, D column)
+  const int q = lane >> 4;  // kernel row (B / A slots 4q..4q+3), channel quarter of D
+  constexpr uint32_t kOob = 0x80000000u;
+  h8* const wl = hstage + wave * WCH;
+  auto swz = [](int g) { return g ^ ((g >> 3) & 7); };
+  const int rl = lane ^ (((lane >> 4) & 1) << 3);  // chunk of the lane in a store
+
+  h4 wa[NB];
+  f4 bias4[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int ch = (j >> 2) * 4 * NB + 4 * b + (j & 3);  // A row j of block b
+    const _Float16* wp = reinterpret_cast<const _Float16*>(a.w) + ch * 10 + 3 * (q < 3 ? q : 0);
+    wa[b] = q < 3 ? h4{wp[0], wp[1], wp[2], (_Float16)0.0f} : h4{0, 0, 0, 0};
+    bias4[b] = *reinterpret_cast<const f4*>(a.epi.bias + q * 4 * NB + 4 * b);
+  }
+
+  const int G = gridDim.x;
+  const int slot = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  const int begin = (int)((int64_t)n_items * slot / G);
+  const int end = (int)((int64_t)n_items * (slot + 1) / G);
+  if (begin >= end) return;
+
+  // Item = (n * n_seg + segment) * H + output row.
+  auto decode = [&](int item, int& n, int& sg, int& y) {
+    const uint32_t t = fdiv((uint32_t)item, fd_H);
+    y = item - (int)(t * (uint32_t)a.H);
+    const uint32_t nn = fdiv(t, fd_seg);
+    sg = (int)(t - nn * (uint32_t)n_seg);
+    n = (int)nn;
+  };
+  constexpr int EB = BIN == 2 ? 4 : 2;  // bytes per input element
+  // B operand of `item`: input (row y - 1 + q, columns x - 1 .. x + 1) of
+  // pixel x, zero outside the image (padded input: the zero border).
+  auto load_b = [&](int item, _Float16 (&v)[3]) {
+    int n, sg, y;
+    decode(item, n, sg, y);
+    const int x = SEG * sg + 16 * wave + j;
+    const int64_t img = BIN ? (int64_t)a.H * a.W : (int64_t)a.Hp * a.Wp;
+    const char* base = reinterpret_cast<const char*>(a.in) + (int64_t)n * img * EB;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(img * EB), 0x00020000);
+#pragma unroll
+    for (int dx = 0; dx < 3; ++dx) {
+      uint32_t o;
+      if (BIN == 0) {
+        // Padded row y + q, column x + dx (x + dx past the row end reads the
+        // next row: such pixels are never stored).
+        o = q < 3 ? (uint32_t)((y + q) * a.Wp + x + dx) * EB : kOob;
+      } else {
+        const int hr = y - 1 + q, c = x - 1 + dx;
+        o = q < 3 && hr >= 0 && hr < a.H && c >= 0 && c < a.W ? (uint32_t)(hr * a.W + c) * EB : kOob;
+      }
+      if (BIN == 2)
+        v[dx] = (_Float16)__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0));
+      else
+        v[dx] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0));
+    }
+  };
+
+  _Float16 cur[3], nxt[3];
+  load_b(begin, cur);
+  for (int it = begin; it < end; ++it) {
+    if (it + 1 < end) load_b(it + 1, nxt);
+    int n, sg, y;
+    decode(it, n, sg, y);
+    const int x0 = SEG * sg;
+    const h4 bv = {cur[0], cur[1], cur[2], (_Float16)0.0f};
+    char* ob = reinterpret_cast<char*>(a.epi.out) + (((int64_t)n * a.Hp + y + 1) * a.Wp + x0 + 1) * M * 2;
+    const int valid = min(SEG, a.W - x0);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, valid * M * 2, 0x00020000);
+#pragma unroll
+    for (int m = 0; m < NB / 2; ++m) {
+      const f4 z = {0, 0, 0, 0};
+      const f4 d0 = __builtin_amdgcn_mfma_f32_16x16x16f16(wa[2 * m], bv, z, 0, 0, 0);
+      const f4 d1 = __builtin_amdgcn_mfma_f32_16x16x16f16(wa[2 * m + 1], bv, z, 0, 0, 0);
+      const h4 zh = {0, 0, 0, 0};
+      const h4 v0 = fast4<ACT>(d0, bias4[2 * m], zh, zh);
+      const h4 v1 = fast4<ACT>(d1, bias4[2 * m + 1], zh, zh);
+      wl[swz(j * CH + q * (NB / 2) + m)] = h8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    }
+    // The wave's block is bytes [16 * wave * M * 2, + 16 * M * 2) of the row
+    // segment; pixels past the image's right edge fall outside the resource.
+    const uint32_t wbase = (uint32_t)(16 * wave * M * 2);
+#pragma unroll
+    for (int st = 0; st < WCH / 64; ++st) {
+      const int g = 64 * st + rl;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, wl[swz(g)]), rs, wbase + 16 * g, 0,
+                                             kNonTemporal);
+    }
+#pragma unroll
+    for (int e = 0; e < 3; ++e) cur[e] = nxt[e];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Elementwise, DepthToSpace and boundary IO (off the fused hot path)
 // ---------------------------------------------------------------------------
@@ -2479,6 +2608,38 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
              direct_conv_c1_walk<GG, kActSilu, false, 2>}};
         return t[variant][act];
       };
+      // M = 32, 64, 96 without residual inputs: the MFMA head.
+      if (!sk && a.M % 32 == 0 && a.M <= 96) {
+        const int ns = (a.W + 63) / 64;
+        const int64_t mitems = (int64_t)a.N * ns * a.H;
+        if (mitems < ((int64_t)1 << 31)) {
+          auto mpick = [&](auto nb_tag) -> HeadKernel {
+            constexpr int NB = decltype(nb_tag)::value;
+            static const HeadKernel t[3][3] = {
+                {direct_conv_c1_mfma<NB, kActNone, 0>, direct_conv_c1_mfma<NB, kActRelu, 0>,
+                 direct_conv_c1_mfma<NB, kActSilu, 0>},
+                {direct_conv_c1_mfma<NB, kActNone, 1>, direct_conv_c1_mfma<NB, kActRelu, 1>,
+                 direct_conv_c1_mfma<NB, kActSilu, 1>},
+                {direct_conv_c1_mfma<NB, kActNone, 2>, direct_conv_c1_mfma<NB, kActRelu, 2>,
+                 direct_conv_c1_mfma<NB, kActSilu, 2>}};
+            return t[a.in_kind][act];
+          };
+          HeadKernel fn = a.M == 32 ? mpick(IntC<2>{}) : a.M == 64 ? mpick(IntC<4>{}) : mpick(IntC<6>{});
+          // Four waves' staging blocks: 16 pixels x M fp16 each.
+          const size_t lds = (size_t)4 * 16 * a.M * 2;
+          int occ = 0;
+          if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn),
+                                                           256, lds) != hipSuccess ||
+              occ < 1)
+            occ = 1;
+          int64_t grid = (int64_t)cu_count() * occ;
+          if (grid > mitems) grid = mitems;
+          grid = (grid + 7) / 8 * 8;
+          const FastDiv fms = make_fastdiv((uint32_t)ns);
+          hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), lds, s, a, ns, (int)mitems, fms, fh);
+          return hipGetLastError();
+        }
+      }
       HeadKernel fn = a.g8 == 1 ? pick(IntC<1>{}) : a.g8 == 2 ? pick(IntC<2>{})
                     : a.g8 == 4 ? pick(IntC<4>{}) : a.g8 == 8 ? pick(IntC<8>{}) : pick(IntC<16>{});
       int occ = 0;

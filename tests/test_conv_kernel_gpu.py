@@ -235,6 +235,21 @@ def test_head_tiny(h, w):
     check(run_conv(x, wt, b, 1), oracle_conv(x, wt, b, 1), f"head {h}x{w}")
 
 
+# The MFMA head (C = 1, M = 32, 64 or 96 without residual inputs; 64-pixel row
+# segments, 16 per wave): every geometry, each activation, a batch of two.
+@pytest.mark.parametrize("m", [32, 64, 96])
+@pytest.mark.parametrize("h,w", GEOMETRY)
+def test_head_mfma_geometry(m, h, w):
+    x, wt, b = make_case(23, 1, 1, m, h, w)
+    check(run_conv(x, wt, b), oracle_conv(x, wt, b), f"head{m} {h}x{w}")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_head_mfma_epilogue_batch(act):
+    x, wt, b = make_case(24, 2, 1, 64, 19, 70)
+    check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"head act{act}")
+
+
 # C == M in {64, 96} without residual inputs runs the producer/consumer kernel
 # (winograd_pipe): the same strips, with the producers' row window restarting
 # at every strip boundary of a workgroup's item range.
@@ -258,8 +273,8 @@ def test_pipe_epilogue_c64(act):
     check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"pipe64 act{act}")
 
 
-# SiLU at 64 channels: the producers apply it in place on a third staging
-# buffer, so the consumers' store trails the fold by two steps (longer tail).
+# SiLU at 64 channels: the consumers apply it in the fold (exp and reciprocal
+# on the critical path), across geometries and a 360x640 frame.
 @pytest.mark.parametrize("h,w", GEOMETRY + TINY + [(360, 640)])
 def test_pipe_silu_c64(h, w):
     x, wt, b = make_case(40, 1, 64, 64, h, w)
