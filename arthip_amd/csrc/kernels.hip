@@ -2586,7 +2586,11 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
     const int seg = 4 * 256 / a.g8;
     const int n_seg = (a.W + seg - 1) / seg;
     const int64_t items = (int64_t)a.N * n_seg * a.H;
-    if (items < ((int64_t)1 << 31)) {
+    // The head kernels address one input image through a buffer resource with
+    // a 32-bit size (NCHW boundary image, or the padded copy).
+    const int64_t in_img = a.in_kind == 0 ? (int64_t)a.Hp * a.Wp * 2
+                                          : (int64_t)a.H * a.W * (a.in_kind == 2 ? 4 : 2);
+    if (items < ((int64_t)1 << 31) && in_img < ((int64_t)1 << 31)) {
       const FastDiv fs = make_fastdiv((uint32_t)n_seg), fh = make_fastdiv((uint32_t)a.H);
       using HeadKernel = void (*)(DirectArgs, int, int, FastDiv, FastDiv);
       const bool sk = a.epi.skip0 != nullptr || a.epi.skip1 != nullptr;
