@@ -29,6 +29,9 @@ extern "C" {
 /* mutex. It replaces vship::HipEngine (src/vapoursynth/hip_engine.h:88-188)  */
 /* and onnxruntime::hip::HipGraph (src/onnxruntime-hip/hip_graph.h:113-167), */
 /* which the VapourSynth plugin and the ONNX Runtime EP each drive.          */
+/* Calls on one handle from several threads are serialized by that mutex (as */
+/* HipGraph::Run's lock, hip_graph.cc:1212); destroy must not overlap any    */
+/* other call on the handle. No entry point lets a C++ exception escape.     */
 /* ------------------------------------------------------------------------ */
 
 typedef struct arthip_engine arthip_engine;
