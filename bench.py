@@ -51,7 +51,7 @@ def parse():
                    help="r8f64 (default, the headline workload); shipped_like: the shipped "
                         "luma model's architecture (SiLU, 3-conv blocks, Clip) with synthetic weights")
     p.add_argument("--batch", type=int, default=1)
-    p.add_argument("--cpu-rows", type=int, default=270,
+    p.add_argument("--cpu-rows", type=int, default=360,
                    help="rows of the frame in the CPU baseline sample (0 disables it)")
     p.add_argument("--no-profile", action="store_true",
                    help="skip the per-launch event timing (roofline becomes null)")
