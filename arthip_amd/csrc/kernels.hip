@@ -662,7 +662,7 @@ winograd_strip(StripArgs a) {
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const h4 v = *reinterpret_cast<const h4*>(rb + r * row_bytes + in_lane + j * PX);
+        const h4 v = __builtin_nontemporal_load(reinterpret_cast<const h4*>(rb + r * row_bytes + in_lane + j * PX));
         x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
         x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
       }
