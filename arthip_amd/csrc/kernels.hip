@@ -1992,7 +1992,9 @@ __global__ void __launch_bounds__(256) direct_conv_c1_walk(DirectArgs a, int n_s
 // instruction s taking 16-byte chunk 64 s + (l ^ 8 for lanes 16-31 and 48-63):
 // whole lines per instruction. LDS operations of one wave complete in order,
 // so the region needs no barrier. Chunk g sits at g ^ ((g >> 3) & 7): the
-// reads are bank-conflict free, the MFMA-layout writes at most 2-way.
+// reads are bank-conflict free, the MFMA-layout writes at most 2-way. The
+// stores are plain, not nontemporal: the next two layers read this output
+// first (1 -> 64 at 1080p: 63 -> 57 us, and the first residual layer gains).
 // An item is one output row x 64 pixels (16 per wave); every lane issues the
 // same loads and stores on every path (out-of-range offsets read zero and drop
 // stores), and the next item's loads go out before this item's MFMAs. The
@@ -2098,8 +2100,7 @@ __global__ void __launch_bounds__(256) direct_conv_c1_mfma(DirectArgs a, int n_s
 #pragma unroll
     for (int st = 0; st < WCH / 64; ++st) {
       const int g = 64 * st + rl;
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, wl[swz(g)]), rs, wbase + 16 * g, 0,
-                                             kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, wl[swz(g)]), rs, wbase + 16 * g, 0, 0);
     }
 #pragma unroll
     for (int e = 0; e < 3; ++e) cur[e] = nxt[e];
