@@ -657,6 +657,9 @@ winograd_strip(StripArgs a) {
   auto in_row = [&](int r) {
     return reinterpret_cast<const char*>(a.in) + (((int64_t)n * a.Hp + r) * a.Wp + 32 * s) * PX;
   };
+  // Input rows are nontemporal: in the model's residual layers nothing reads
+  // them again, and bypassing the caches keeps the residual input (which the
+  // previous layer just read) cached (1080p 64 -> 64: 152 -> 146 us).
   auto load2 = [&](h2 (&x)[16], const char* rb) {
 #pragma unroll
     for (int r = 0; r < 2; ++r)
