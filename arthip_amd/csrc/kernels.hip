@@ -940,7 +940,10 @@ winograd_pipe(StripArgs a) {
   using LL = PipeL<KC>;
   constexpr int C = L::C;
   constexpr int NCW = L::NCW;
-  constexpr int NW = LL::NW;
+  // With two residual inputs at C = 96 the producers' 3-slot row ring and
+  // residual registers exceed 256 VGPRs and spill; a 2-slot ring does not
+  // (1080p: 378 -> 327 us). Shallower rings elsewhere measured slower.
+  constexpr int NW = (KC == 3 && NSKIP == 2) ? 2 : LL::NW;
   constexpr int UP = L::UP;
   constexpr int WPS = L::WPS;
   constexpr int VBUF = L::VBUF;
