@@ -78,6 +78,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_engine_set_profiling", c_int, eng, c_int)
     sig("arthip_engine_profile_read", c_int, eng, c_int, ctypes.POINTER(ctypes.c_double), i64p,
         c_char, c_int, c_char, c_int)
+    sig("arthip_engine_set_debug", c_int, eng, c_int, c_char)
+    sig("arthip_engine_get_debug", c_int, eng, i32p)
 
     sig("engine_device_count", c_int, i32p)
     sig("engine_probe", c_int, c_char, c_int, c_int, c_int, c_int, c_int, c_char, c_int,
@@ -124,7 +126,8 @@ EXPORTED_SYMBOLS = (
     "arthip_engine_create", "arthip_engine_destroy", "arthip_engine_build_file",
     "arthip_engine_build_bytes", "arthip_engine_output_shape", "arthip_engine_io_info",
     "arthip_engine_run", "arthip_engine_run_device", "arthip_engine_describe",
-    "arthip_engine_set_profiling", "arthip_engine_profile_read",
+    "arthip_engine_set_profiling", "arthip_engine_profile_read", "arthip_engine_set_debug",
+    "arthip_engine_get_debug",
     "engine_device_count", "engine_probe", "engine_run", "engine_alloc_failure_then_run",
     "arthip_ep_get_capability", "arthip_ep_run_boundary", "arthip_engine_build_subgraph",
     "arthip_vs_model_create", "arthip_vs_model_get_frame", "arthip_vs_model_destroy",

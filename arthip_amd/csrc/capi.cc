@@ -197,6 +197,24 @@ int arthip_engine_set_profiling(arthip_engine* eng, int on) {
   return ARTHIP_OK;
 }
 
+int arthip_engine_set_debug(arthip_engine* eng, int flags, const char* dump_dir) {
+  return guard(ARTHIP_ERR_BUILD, nullptr, 0, "", [&]() -> int {
+    if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);
+    if ((flags & ~(ARTHIP_DEBUG_POISON | ARTHIP_DEBUG_SYNC_EACH | ARTHIP_DEBUG_DUMP)) != 0)
+      return fail("unknown debug flag", ARTHIP_ERR_BUILD);
+    if ((flags & ARTHIP_DEBUG_DUMP) && (dump_dir == nullptr || *dump_dir == '\0'))
+      return fail("dump requested without a directory", ARTHIP_ERR_BUILD);
+    eng->eng->SetDebug(flags, dump_dir ? dump_dir : "");
+    return ARTHIP_OK;
+  });
+}
+
+int arthip_engine_get_debug(const arthip_engine* eng, int* flags) {
+  if (eng == nullptr || flags == nullptr) return fail("null argument", ARTHIP_ERR_BUILD);
+  *flags = eng->eng->DebugFlags();
+  return ARTHIP_OK;
+}
+
 int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_ms,
                                int64_t* launches, char* names, int names_len, char* err,
                                int errlen) {

@@ -1,12 +1,15 @@
 #include "engine.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 
 #include "half.h"
 #include "launch.h"
 #include "pack.h"
+#include "plan_rules.h"
 
 namespace arthip {
 
@@ -23,7 +26,20 @@ size_t PaddedBytes(const Shape& s) {
 
 }  // namespace
 
-Engine::Engine(int device_id) : device_(device_id) {}
+Engine::Engine(int device_id) : device_(device_id) {
+  auto on = [](const char* name) {
+    const char* e = std::getenv(name);
+    return e != nullptr && *e == '1';
+  };
+  if (on("VSHIP_POISON")) debug_ |= kDebugPoison;
+  if (on("VSHIP_SYNC_EACH")) debug_ |= kDebugSyncEach;
+  if (const char* d = std::getenv("VSHIP_DUMP")) {
+    if (*d != '\0') {
+      debug_ |= kDebugDump;
+      dump_dir_ = d;
+    }
+  }
+}
 
 Engine::~Engine() {
   FreeAll();
@@ -36,6 +52,40 @@ Engine::~Engine() {
     hipSetDevice(device_);
     hipStreamDestroy(stream_);
   }
+  if (run_done_) hipEventDestroy(run_done_);
+}
+
+void Engine::SetDebug(int flags, const std::string& dump_dir) {
+  std::lock_guard<std::mutex> lock(mu_);
+  debug_ = flags & (kDebugPoison | kDebugSyncEach | kDebugDump);
+  dump_dir_ = dump_dir;
+  dump_runs_ = 0;
+}
+
+int Engine::DebugFlags() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return debug_;
+}
+
+// The previous run may still be executing on another stream; this run reuses
+// its activation buffers, so its first launch waits for that run's event.
+bool Engine::WaitPrevious(hipStream_t s, std::string& error) {
+  if (last_stream_ == nullptr || last_stream_ == s) return true;
+  const hipError_t e = hipStreamWaitEvent(s, run_done_, 0);
+  if (e != hipSuccess) {
+    error = HipErr("hipStreamWaitEvent on the previous run", e);
+    return false;
+  }
+  return true;
+}
+
+// Blocks until the last enqueued run has finished (before its buffers are
+// freed or replaced).
+bool Engine::DrainPrevious() {
+  if (last_stream_ == nullptr) return true;
+  const hipError_t e = hipEventSynchronize(run_done_);
+  last_stream_ = nullptr;
+  return e == hipSuccess;
 }
 
 bool Engine::SetDevice(std::string& error) const {
@@ -55,12 +105,19 @@ bool Engine::Init(std::string& error) {
     return false;
   }
   if (!SetDevice(error)) return false;
-  if (stream_ == nullptr) {
-    const hipError_t e = hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking);
+  if (run_done_ == nullptr) {
+    const hipError_t e = hipEventCreateWithFlags(&run_done_, hipEventDisableTiming);
     if (e != hipSuccess) {
-      error = HipErr("hipStreamCreate", e);
+      run_done_ = nullptr;
+      error = HipErr("hipEventCreate", e);
       return false;
     }
+  }
+  const hipError_t e = hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    stream_ = nullptr;
+    error = HipErr("hipStreamCreate", e);
+    return false;
   }
   return true;
 }
@@ -96,19 +153,36 @@ bool Engine::BuildParsed(const onnx::Model& model, std::string& error, const Bui
   return true;
 }
 
+bool Engine::InputFp32() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return graph_.input_fp32;
+}
+
+bool Engine::OutputFp32() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return graph_.output_fp32;
+}
+
 int Engine::InputChannels() const {
+  std::lock_guard<std::mutex> lock(mu_);
   for (const Op& op : graph_.ops)
     if (op.kind == OpKind::Conv) return static_cast<int>(graph_.weights.at(op.weight).dims[1]);
   return 1;
 }
 
 int Engine::OutputChannels() const {
+  std::lock_guard<std::mutex> lock(mu_);
   for (auto it = graph_.ops.rbegin(); it != graph_.ops.rend(); ++it)
     if (it->kind == OpKind::Conv) return static_cast<int>(graph_.weights.at(it->weight).dims[0]);
   return 1;
 }
 
 bool Engine::OutputShape(const int64_t in[4], int64_t out[4]) const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return OutputShapeUnlocked(in, out);
+}
+
+bool Engine::OutputShapeUnlocked(const int64_t in[4], int64_t out[4]) const {
   if (!built_) return false;
   std::unordered_map<std::string, Shape> shapes;
   if (!PropagateShapes(graph_, in, shapes)) return false;
@@ -121,12 +195,18 @@ bool Engine::OutputShape(const int64_t in[4], int64_t out[4]) const {
 }
 
 size_t Engine::InputBytes(const int64_t in[4]) const {
+  std::lock_guard<std::mutex> lock(mu_);
   return static_cast<size_t>(in[0] * in[1] * in[2] * in[3]) * (graph_.input_fp32 ? 4 : 2);
 }
 
 size_t Engine::OutputBytes(const int64_t in[4]) const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return OutputBytesUnlocked(in);
+}
+
+size_t Engine::OutputBytesUnlocked(const int64_t in[4]) const {
   int64_t o[4];
-  if (!OutputShape(in, o)) return 0;
+  if (!OutputShapeUnlocked(in, o)) return 0;
   return static_cast<size_t>(o[0] * o[1] * o[2] * o[3]) * (graph_.output_fp32 ? 4 : 2);
 }
 
@@ -134,6 +214,7 @@ void Engine::FreePlan() {
   prof_acc_.clear();
   const bool any = !bufs_.empty() || in_stage_dev_ || out_stage_dev_ || in_pinned_ || out_pinned_;
   if (any) hipSetDevice(device_);  // frees need the owning device current on this thread
+  DrainPrevious();  // the last run may still read or write these buffers
   for (auto& b : bufs_)
     if (b.ptr) hipFree(b.ptr);
   bufs_.clear();
@@ -151,6 +232,7 @@ void Engine::FreePlan() {
 void Engine::FreeAll() {
   FreePlan();
   if (!wbufs_.empty()) hipSetDevice(device_);
+  DrainPrevious();
   for (auto& b : wbufs_)
     if (b.ptr) hipFree(b.ptr);
   wbufs_.clear();
@@ -281,6 +363,7 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
     }
     DevBuf b;
     b.bytes = PaddedBytes(s);
+    b.geo = s;
     const hipError_t e = hipMalloc(&b.ptr, b.bytes);
     if (e != hipSuccess) {
       error = "hipMalloc of " + std::to_string(b.bytes) + " bytes for tensor '" + name +
@@ -325,8 +408,8 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
       const Op& op = ops[reader];
       const int64_t m = graph_.weights.at(op.weight).dims[0];
       const bool to_boundary = direct_out && reader == final_op;
-      if (!to_boundary && m % 8 == 0 && m <= 128 && !op.clip && op.dts_b < 1 && op.skips.empty() &&
-          sin.n * sin.h * ((sin.w + 1023) / 4) < ((int64_t)1 << 31))
+      if (!to_boundary && !op.clip && op.dts_b < 1 && op.skips.empty() &&
+          head_reads_boundary_input(sin.n, sin.h, sin.w, m, graph_.input_fp32))
         fused_in_op = reader;
     }
   }
@@ -425,8 +508,8 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
     steps_.push_back(st);
   }
 
-  in_bytes_ = InputBytes(in);
-  out_bytes_ = OutputBytes(in);
+  in_bytes_ = static_cast<size_t>(in[0] * in[1] * in[2] * in[3]) * (graph_.input_fp32 ? 4 : 2);
+  out_bytes_ = OutputBytesUnlocked(in);
   hipError_t e = hipStreamSynchronize(stream_);  // buffer zeroing done
   if (e != hipSuccess) {
     error = HipErr("hipStreamSynchronize after plan setup", e);
@@ -444,10 +527,47 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
     if (idx < 0) return nullptr;
     return bufs_[idx].ptr;
   };
+  auto bytes_of = [&](int idx) -> size_t {
+    if (idx == kBoundaryIn) return in_bytes_;
+    if (idx == kBoundaryOut) return out_bytes_;
+    if (idx < 0) return 0;
+    return bufs_[idx].bytes;
+  };
   if (profiling_ && prof_acc_.size() != steps_.size()) {
     prof_acc_.assign(steps_.size(), StepProfile{});
     for (size_t i = 0; i < steps_.size(); ++i) prof_acc_[i].name = StepName(steps_[i]);
   }
+  if (!WaitPrevious(s, error)) return false;
+  // From here on the run's work is on s: later runs order after it even when
+  // this one fails part way.
+  last_stream_ = s;
+  auto finish = [&](bool ok) -> bool {
+    const hipError_t r = hipEventRecord(run_done_, s);
+    if (r != hipSuccess && ok) {
+      error = HipErr("hipEventRecord at the end of a run", r);
+      return false;
+    }
+    return ok;
+  };
+
+  // VSHIP_POISON: every activation interior becomes fp16 NaN (0x7E7E), the
+  // reference's poison pattern; the zero border stays. A launch that reads a
+  // tensor no earlier launch of this run wrote then yields NaN.
+  if (debug_ & kDebugPoison) {
+    for (const DevBuf& b : bufs_) {
+      const hipError_t e = launch_poison(b.ptr, (int32_t)b.geo.n, (int32_t)b.geo.h,
+                                         (int32_t)b.geo.w, (int32_t)b.geo.c, 0x7E7E, s);
+      if (e != hipSuccess) {
+        error = HipErr("poison fill", e);
+        return finish(false);
+      }
+    }
+  }
+  // VSHIP_DUMP: each launch's inputs and output as raw files, for the first
+  // two runs of the engine. Activations are padded NHWC fp16 buffers.
+  const bool dump = (debug_ & kDebugDump) != 0 && !dump_dir_.empty() && dump_runs_ < 2;
+  const uint64_t dump_run = dump ? ++dump_runs_ : 0;
+
   for (size_t i = 0; i < steps_.size(); ++i) {
     const Step& st = steps_[i];
     hipError_t e = hipSuccess;
@@ -457,7 +577,7 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
       ev.stop = TakeEvent();
       if (ev.start == nullptr || ev.stop == nullptr || hipEventRecord(ev.start, s) != hipSuccess) {
         error = "HIP event creation/record for profiling failed";
-        return false;
+        return finish(false);
       }
     }
     switch (st.kind) {
@@ -532,17 +652,55 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
     if (e != hipSuccess) {
       error = "HIP kernel launch for step " + std::to_string(i) + " failed: " +
               hipGetErrorString(e);
-      return false;
+      return finish(false);
     }
     if (profiling_) {
       if (hipEventRecord(ev.stop, s) != hipSuccess) {
         error = "HIP event record for profiling failed";
-        return false;
+        return finish(false);
       }
       pending_events_.push_back(ev);
     }
+    if (debug_ & kDebugSyncEach) {
+      const hipError_t se = hipStreamSynchronize(s);
+      if (se != hipSuccess) {
+        error = HipErr(("sync-each after step " + std::to_string(i)).c_str(), se);
+        return finish(false);
+      }
+    }
+    if (dump) {
+      const int ins[4] = {st.in, st.in2, st.skip[0], st.skip[1]};
+      int k = 0;
+      char path[4096];
+      for (int idx : ins) {
+        if (idx == kNoBuffer) continue;
+        std::snprintf(path, sizeof(path), "%s/run%llu_op%02zu_in%d.bin", dump_dir_.c_str(),
+                      (unsigned long long)dump_run, i, k++);
+        if (!Dump(path, ptr(idx), bytes_of(idx), s)) {
+          error = std::string("dump of ") + path + " failed";
+          return finish(false);
+        }
+      }
+      std::snprintf(path, sizeof(path), "%s/run%llu_op%02zu_out.bin", dump_dir_.c_str(),
+                    (unsigned long long)dump_run, i);
+      if (!Dump(path, ptr(st.out), bytes_of(st.out), s)) {
+        error = std::string("dump of ") + path + " failed";
+        return finish(false);
+      }
+    }
   }
-  return true;
+  return finish(true);
+}
+
+bool Engine::Dump(const std::string& path, const void* dev, size_t bytes, hipStream_t s) {
+  std::vector<uint8_t> host(bytes);
+  hipError_t e = hipMemcpyAsync(host.data(), dev, bytes, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return false;
+  FILE* f = std::fopen(path.c_str(), "wb");
+  if (f == nullptr) return false;
+  const bool ok = std::fwrite(host.data(), 1, bytes, f) == bytes;
+  return std::fclose(f) == 0 && ok;
 }
 
 hipEvent_t Engine::TakeEvent() {

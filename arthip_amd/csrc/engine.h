@@ -25,6 +25,16 @@ namespace arthip {
 struct DevBuf {
   void* ptr = nullptr;
   size_t bytes = 0;
+  Shape geo{};  // activation buffers: the tensor geometry (padded NHWC around it)
+};
+
+// Diagnostics, the reference's environment switches (hip_engine.cc:1310-1349,
+// hip_graph.cc:1231-1248,1356-1365). An engine starts from VSHIP_POISON=1,
+// VSHIP_SYNC_EACH=1 and VSHIP_DUMP=<dir>; SetDebug overrides them.
+enum DebugFlag : int {
+  kDebugPoison = 1,    // before each run, fill every activation interior with fp16 NaN
+  kDebugSyncEach = 2,  // synchronize the launch stream after every launch
+  kDebugDump = 4,      // write each launch's inputs and output (first two runs)
 };
 
 enum class StepKind { InputConvert, ConvWinograd, ConvDirect, Eltwise, DepthToSpace, OutputConvert };
@@ -72,8 +82,8 @@ class Engine {
                    const BuildOptions& opts = BuildOptions());
 
   bool OutputShape(const int64_t in_nchw[4], int64_t out_nchw[4]) const;
-  bool InputFp32() const { return graph_.input_fp32; }
-  bool OutputFp32() const { return graph_.output_fp32; }
+  bool InputFp32() const;
+  bool OutputFp32() const;
   // First conv's input channels / last conv's output channels (before a
   // trailing DepthToSpace), as the reference reports them (hip_engine.h:127-136).
   int InputChannels() const;
@@ -81,8 +91,17 @@ class Engine {
 
   bool Run(const void* in_host, const int64_t in_nchw[4], void* out_host, size_t out_cap,
            std::string& error);
+  // RunDevice enqueues on `stream` (null: the engine's stream) and returns
+  // without waiting. Runs on one engine share its activation buffers, so each
+  // run's launches are ordered after the previous run's, whatever streams the
+  // two were given (an event recorded at the end of every run, waited on by
+  // the next run's stream when it differs).
   bool RunDevice(const void* in_dev, const int64_t in_nchw[4], void* out_dev, hipStream_t stream,
                  std::string& error);
+
+  // Diagnostics (DebugFlag bits); dump_dir is used with kDebugDump.
+  void SetDebug(int flags, const std::string& dump_dir);
+  int DebugFlags() const;
 
   std::string Describe() const;
 
@@ -102,6 +121,8 @@ class Engine {
 
  private:
   bool SetDevice(std::string& error) const;
+  bool OutputShapeUnlocked(const int64_t in_nchw[4], int64_t out_nchw[4]) const;
+  size_t OutputBytesUnlocked(const int64_t in_nchw[4]) const;
   bool EnsurePlan(const int64_t in_nchw[4], std::string& error);
   bool EnsureWeights(std::string& error);
   bool Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::string& error);
@@ -110,6 +131,16 @@ class Engine {
 
   int device_;
   hipStream_t stream_ = nullptr;
+  // Completion of the last enqueued run and the stream it went to.
+  hipEvent_t run_done_ = nullptr;
+  hipStream_t last_stream_ = nullptr;
+  bool WaitPrevious(hipStream_t s, std::string& error);
+  bool DrainPrevious();
+
+  int debug_ = 0;
+  std::string dump_dir_;
+  uint64_t dump_runs_ = 0;
+  bool Dump(const std::string& path, const void* dev, size_t bytes, hipStream_t s);
   Graph graph_;
   bool built_ = false;
 

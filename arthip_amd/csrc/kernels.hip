@@ -37,6 +37,7 @@
 
 #include "conv_args.h"
 #include "pack.h"
+#include "plan_rules.h"
 
 namespace arthip {
 
@@ -2233,6 +2234,25 @@ __global__ void __launch_bounds__(256) output_convert(IoArgs a) {
   }
 }
 
+// Diagnostic fill of a padded NHWC fp16 buffer's interior (rows 1..H, columns
+// 1..W, every channel) with one 16-bit pattern; the zero border is not
+// touched. One thread per interior element.
+__global__ void __launch_bounds__(256) poison_interior(uint16_t* buf, int32_t N, int32_t H,
+                                                       int32_t W, int32_t C, int32_t Hp,
+                                                       int32_t Wp, uint32_t pattern) {
+  const int64_t total = (int64_t)N * H * W * C;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % C);
+    int64_t r = i / C;
+    const int w = (int)(r % W);
+    r /= W;
+    const int h = (int)(r % H);
+    const int64_t n = r / H;
+    buf[((n * Hp + h + 1) * Wp + w + 1) * C + c] = (uint16_t)pattern;
+  }
+}
+
 // VapourSynth plane samples <-> NCHW boundary elements, one element per
 // thread step (src/vapoursynth/vs_hip.cpp:175-225 packs on the host,
 // 347-369 unpacks integer output):
@@ -2567,11 +2587,7 @@ hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
   return hipGetLastError();
 }
 
-int direct_g8(int M) {
-  int g = 1;
-  while (g * 8 < M) g *= 2;
-  return g;
-}
+int direct_g8(int M) { return head_g8(M); }
 
 hipError_t launch_direct(DirectArgs a, hipStream_t s) {
   // Only the column-walking fast path reads the NCHW boundary input; the
@@ -2594,10 +2610,12 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s) {
     const int n_seg = (a.W + seg - 1) / seg;
     const int64_t items = (int64_t)a.N * n_seg * a.H;
     // The head kernels address one input image through a buffer resource with
-    // a 32-bit size (NCHW boundary image, or the padded copy).
-    const int64_t in_img = a.in_kind == 0 ? (int64_t)a.Hp * a.Wp * 2
-                                          : (int64_t)a.H * a.W * (a.in_kind == 2 ? 4 : 2);
-    if (items < ((int64_t)1 << 31) && in_img < ((int64_t)1 << 31)) {
+    // a 32-bit size (NCHW boundary image, or the padded copy). For the boundary
+    // input the planner applies the same rule (head_reads_boundary_input).
+    const bool fits = a.in_kind == 0
+                          ? items < ((int64_t)1 << 31) && (int64_t)a.Hp * a.Wp * 2 < ((int64_t)1 << 31)
+                          : head_reads_boundary_input(a.N, a.H, a.W, a.M, a.in_kind == 2);
+    if (fits) {
       const FastDiv fs = make_fastdiv((uint32_t)n_seg), fh = make_fastdiv((uint32_t)a.H);
       using HeadKernel = void (*)(DirectArgs, int, int, FastDiv, FastDiv);
       const bool sk = a.epi.skip0 != nullptr || a.epi.skip1 != nullptr;
@@ -2698,6 +2716,17 @@ hipError_t launch_input_convert(IoArgs a, hipStream_t s) {
 hipError_t launch_output_convert(IoArgs a, hipStream_t s) {
   const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
   hipLaunchKernelGGL(output_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_poison(void* buf, int32_t N, int32_t H, int32_t W, int32_t C, uint16_t pattern,
+                         hipStream_t s) {
+  if (buf == nullptr || N < 0 || H < 0 || W < 0 || C < 0) return hipErrorInvalidValue;
+  const int64_t total = (int64_t)N * H * W * C;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(poison_interior, dim3(grid_for(total, 256)), dim3(256), 0, s,
+                     static_cast<uint16_t*>(buf), N, H, W, C, (int32_t)padded_rows(H),
+                     (int32_t)padded_cols(W), (uint32_t)pattern);
   return hipGetLastError();
 }
 

@@ -19,5 +19,9 @@ hipError_t launch_dts(DtsArgs a, hipStream_t s);
 hipError_t launch_input_convert(IoArgs a, hipStream_t s);
 hipError_t launch_output_convert(IoArgs a, hipStream_t s);
 hipError_t launch_plane_convert(PlaneArgs a, hipStream_t s);
+// Fills the interior of a padded NHWC fp16 buffer holding an N x H x W x C
+// tensor with `pattern` (diagnostics); the border keeps its zeros.
+hipError_t launch_poison(void* buf, int32_t N, int32_t H, int32_t W, int32_t C, uint16_t pattern,
+                         hipStream_t s);
 
 }  // namespace arthip

@@ -68,10 +68,15 @@ int arthip_engine_run(arthip_engine* eng, const void* in_host, const int64_t in_
                       void* out_host, size_t out_cap, char* err, int errlen);
 
 /* The same with device-resident IO on a caller stream (NULL = the engine's
- * stream). No host copies and no synchronisation: the caller orders work on
- * the stream. The reference has no counterpart (its Run always stages through
- * host memory); this is the entry point for callers whose frames already live
- * in HBM. */
+ * stream). No host copies and no host synchronisation: the caller orders its
+ * own producers of in_dev and consumers of out_dev on that stream. Runs on
+ * one handle share its intermediate buffers, so the engine orders each run
+ * (run or run_device) after the previous one on the GPU, whatever streams
+ * they were given (an event at the end of every run; the next run's stream
+ * waits on it when the stream differs). The reference has no counterpart (its
+ * Run always stages through host memory and serializes on its one stream,
+ * hip_engine.cc:1282); this is the entry point for callers whose frames
+ * already live in HBM. */
 int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64_t in_nchw[4],
                              void* out_dev, void* stream, char* err, int errlen);
 
@@ -88,6 +93,27 @@ int arthip_engine_set_profiling(arthip_engine* eng, int on);
 int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_ms,
                                int64_t* launches, char* names, int names_len, char* err,
                                int errlen);
+
+/* Diagnostics: the reference's VSHIP_POISON (hip_engine.cc:1310-1323,
+ * hip_graph.cc:1231-1248), VSHIP_SYNC_EACH (hip_graph.cc:1356-1365) and
+ * VSHIP_DUMP (hip_engine.cc:1325-1349, 1509-1519). A new engine takes them
+ * from those environment variables ("1", or a directory for VSHIP_DUMP);
+ * set_debug replaces them.
+ * - POISON: before each run, every internal activation's interior is filled
+ *   with fp16 NaN (0x7E7E); the zero border of the padded layout stays. A
+ *   read of a tensor no launch of the run has written turns into NaN.
+ * - SYNC_EACH: the launch stream is synchronized after every launch and its
+ *   status checked.
+ * - DUMP: for the engine's first two runs, every launch's input buffers and
+ *   output buffer are written to dump_dir/runR_opKK_inI.bin and
+ *   runR_opKK_out.bin (raw bytes; internal activations in the padded NHWC
+ *   fp16 layout of arthip_padded_dims, boundary tensors as given).
+ * Returns 1 on an unknown flag or DUMP without a directory. */
+#define ARTHIP_DEBUG_POISON 1
+#define ARTHIP_DEBUG_SYNC_EACH 2
+#define ARTHIP_DEBUG_DUMP 4
+int arthip_engine_set_debug(arthip_engine* eng, int flags, const char* dump_dir);
+int arthip_engine_get_debug(const arthip_engine* eng, int* flags);
 
 /* ------------------------------------------------------------------------ */
 /* ONNX Runtime execution provider: partitioning and compile                  */

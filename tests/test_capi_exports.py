@@ -10,6 +10,7 @@ import re
 from pathlib import Path
 
 import numpy as np
+import pytest
 
 from arthip_amd import _lib
 from oracle import ops as orc
@@ -144,3 +145,78 @@ def test_narrow_pack_layout():
                     elif col < m_out:
                         want[:, k, lane, e] = w[col, ch].reshape(9)
         np.testing.assert_array_equal(nb, want)
+
+
+def test_debug_switches_without_a_gpu(tmp_path, monkeypatch):
+    """set_debug / get_debug and the VSHIP_* environment switches need no device."""
+    from arthip_amd.engine import Engine, EngineError
+    for var in ("VSHIP_POISON", "VSHIP_SYNC_EACH", "VSHIP_DUMP"):
+        monkeypatch.delenv(var, raising=False)
+    e = Engine(0)
+    assert e.debug_flags() == 0
+    e.set_debug(Engine.DEBUG_POISON | Engine.DEBUG_DUMP, tmp_path)
+    assert e.debug_flags() == 5
+    with pytest.raises(EngineError):
+        e.set_debug(8)
+    with pytest.raises(EngineError):
+        e.set_debug(Engine.DEBUG_DUMP)  # no directory
+    e.set_debug(0)
+    assert e.debug_flags() == 0
+    e.close()
+    monkeypatch.setenv("VSHIP_POISON", "1")
+    monkeypatch.setenv("VSHIP_SYNC_EACH", "1")
+    monkeypatch.setenv("VSHIP_DUMP", str(tmp_path))
+    e = Engine(0)
+    assert e.debug_flags() == 7
+    e.close()
+    monkeypatch.setenv("VSHIP_POISON", "0")
+    monkeypatch.delenv("VSHIP_SYNC_EACH")
+    monkeypatch.setenv("VSHIP_DUMP", "")
+    e = Engine(0)
+    assert e.debug_flags() == 0
+    e.close()
+
+
+HEAD_RULE_PROBE = r"""
+#include <cstdio>
+#include <cstdlib>
+#include "plan_rules.h"
+int main(int argc, char** argv) {
+  for (int i = 1; i + 4 < argc; i += 5) {
+    const long long n = atoll(argv[i]), h = atoll(argv[i + 1]), w = atoll(argv[i + 2]),
+                    m = atoll(argv[i + 3]), f = atoll(argv[i + 4]);
+    std::printf("%d\n", arthip::head_reads_boundary_input(n, h, w, m, f != 0) ? 1 : 0);
+  }
+  return 0;
+}
+"""
+
+
+def test_head_boundary_input_rule(tmp_path):
+    """The planner binds the NCHW boundary input to the head conv only where the
+    head kernels accept it (one predicate, plan_rules.h, used by both): M a
+    multiple of 8 up to 128, work items N * ceil(W / (1024 / g8)) * H and one
+    input image's bytes below 2^31. Compiled with g++ and checked against the
+    rule's boundaries."""
+    import subprocess
+    csrc = Path(__file__).resolve().parents[1] / "arthip_amd" / "csrc"
+    src = tmp_path / "probe.cc"
+    src.write_text(HEAD_RULE_PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", str(csrc), str(src), "-o", str(exe)],
+                   check=True)
+    cases = [
+        ((1, 1080, 1920, 64, 0), 1), ((1, 1080, 1920, 96, 1), 1), ((2, 2160, 3840, 64, 0), 1),
+        ((1, 1080, 1920, 12, 0), 0), ((1, 1080, 1920, 136, 0), 0), ((1, 1080, 1920, 128, 0), 1),
+        ((1, 1080, 1920, 8, 0), 1), ((0, 10, 10, 64, 0), 0),
+        # one fp16 image of 2^31 bytes is refused, one pixel row less is not
+        ((1, 32768, 32768, 64, 0), 0), ((1, 32767, 32768, 64, 0), 1),
+        # fp32: the limit is 2^29 pixels
+        ((1, 16384, 32768, 64, 1), 0), ((1, 16383, 32768, 64, 1), 1),
+        # work items: M = 128 -> g8 = 16, 64-pixel segments; 2^31 items refused
+        ((2 ** 21, 1024, 64, 128, 0), 0), ((2 ** 21 - 1, 1024, 64, 128, 0), 1),
+    ]
+    args = [str(v) for c, _ in cases for v in c]
+    out = subprocess.run([str(exe)] + args, check=True, capture_output=True, text=True).stdout
+    got = [int(v) for v in out.split()]
+    assert got == [want for _, want in cases], list(zip(cases, got))

@@ -5,7 +5,7 @@ pin on the oracle and on the model builders' seeds).
 GPU: the HIP engine against the same vectors: max-abs <= 2e-2 and PSNR >= 50 dB
 (peak 1) where the output range allows (C4F32, single layer, the shipped luma
 model whose Clip bounds outputs to [0, 1]); for the deep He-normal R8F64
-(outputs ~+-200) relative RMS within 4x of the fp16-storage floor.
+(outputs ~+-200) relative RMS within 3x of the fp16-storage floor.
 """
 
 from __future__ import annotations
@@ -60,4 +60,4 @@ def test_engine_matches_golden(name):
         rms = np.sqrt(np.mean(y ** 2))
         rel = np.sqrt(np.mean((got - y) ** 2)) / rms
         floor = np.sqrt(np.mean((y - y32) ** 2)) / rms
-        assert rel <= max(4 * floor, 2e-3), (rel, floor)
+        assert rel <= max(3 * floor, 2e-3), (rel, floor)

@@ -2,11 +2,18 @@
 
 The oracle (oracle/model.py) evaluates the same ONNX model node by node in fp32
 with fp16 tensors between nodes -- ONNX Runtime CPU EP semantics for an fp16
-model. Gates: max-abs <= 2e-2 and PSNR >= 50 dB (peak 1)
-where the configuration's output range allows it (C4F32, the single layer);
-for the deep He-normal models the fp16-storage floor of the model itself is
-far above that (outputs span ~+-200), so those are gated on relative RMS error
-against the floor measured in the same test.
+model. Whether ONNX Runtime keeps fp32 between nodes instead is not pinned
+(no ONNX Runtime here), so the literal gates are checked against both oracle
+modes: fp16 storage per node and fp32 throughout.
+
+Gates:
+- max-abs <= 2e-2 and PSNR >= 50 dB (peak 1) where the configuration's output
+  range allows it (C4F32, the single layer, the shipped luma model); the
+  shipped model is also held to max-abs <= 1.34e-3, the reference's accuracy
+  against ONNX Runtime CPU at 1920x1080 (NOTES.md:78-79);
+- for the deep He-normal models the fp16-storage floor of the model itself is
+  far above that (outputs span ~+-200), so those are gated on relative RMS
+  error <= 3x the floor measured in the same test (the engine measures ~2x).
 """
 
 from __future__ import annotations
@@ -22,6 +29,11 @@ from tests import reference_math as ref
 pytestmark = pytest.mark.gpu
 
 
+#: Deep models: engine relative RMS error against the oracle, as a multiple of
+#: the model's own fp16-storage floor (oracle fp16 storage vs fp32 throughout).
+FLOOR_RATIO = 3.0
+
+
 def _compare(got, want):
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
@@ -31,16 +43,22 @@ def _compare(got, want):
             "rel_rms": float(np.sqrt(np.mean(err ** 2))) / rms}
 
 
+def _literal_gate(got, model, x, label, max_abs=2e-2):
+    """max-abs and PSNR (peak 1) against the oracle in both modes."""
+    for mode in (True, False):
+        want = run_model(model, x, round_fp16=mode)
+        s = _compare(got, want)
+        print(label, "fp16 storage" if mode else "fp32 throughout", s)
+        assert s["max_abs"] <= max_abs and s["psnr"] >= 50.0, (mode, s)
+
+
 def test_c4f32_full_size_meets_gate():
     spec = models.c4f32(seed=0)
     x = models.synthetic_input((1, 1, 540, 960), seed=1)
     with Engine(0) as e:
         got = e.build(spec).run(x).astype(np.float32)
-    want = run_model(spec.model, x)
-    s = _compare(got, want)
-    print("c4f32", s)
     assert got.shape == (1, 1, 1080, 1920)
-    assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
+    _literal_gate(got, spec.model, x, "c4f32 540x960")
 
 
 def test_single_layer_meets_gate():
@@ -48,10 +66,19 @@ def test_single_layer_meets_gate():
     x = models.synthetic_input((1, 64, 270, 480), seed=1, kind="normal")
     with Engine(0) as e:
         got = e.build(spec).run(x).astype(np.float32)
-    want = run_model(spec.model, x)
-    s = _compare(got, want)
-    print("single64", s)
-    assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
+    _literal_gate(got, spec.model, x, "single64 270x480")
+
+
+def test_single_layer_full_size():
+    """The single-layer config at its stated size, 1x64x1080x1920 N(0, 0.5): the
+    whole frame against the oracle in both modes (one conv, so the oracle is
+    cheap enough for the full frame)."""
+    spec = models.single64(seed=0)
+    x = models.synthetic_input((1, 64, 1080, 1920), seed=1, kind="normal")
+    with Engine(0) as e:
+        got = e.build(spec).run(x).astype(np.float32)
+    assert got.shape == (1, 64, 1080, 1920) and np.isfinite(got).all()
+    _literal_gate(got, spec.model, x, "single64 1080x1920")
 
 
 @pytest.mark.parametrize("builder,hw", [(models.r8f64, (48, 80)), (models.shipped_like, (40, 72)),
@@ -65,9 +92,10 @@ def test_deep_models_within_fp16_floor(builder, hw):
     exact = run_model(spec.model, x, round_fp16=False)  # fp32 throughout
     s = _compare(got, want)
     floor = _compare(want, exact)
-    print(spec.name, "engine vs oracle", s, "| oracle fp16 vs fp32 floor", floor)
+    print(spec.name, "engine vs oracle", s, "| oracle fp16 vs fp32 floor", floor,
+          "| ratio", s["rel_rms"] / floor["rel_rms"])
     assert np.isfinite(got).all()
-    assert s["rel_rms"] <= max(4 * floor["rel_rms"], 2e-3), (s, floor)
+    assert s["rel_rms"] <= max(FLOOR_RATIO * floor["rel_rms"], 2e-3), (s, floor)
 
 
 def test_r8f64_batch_two():
@@ -95,15 +123,26 @@ def test_fresh_engines_bit_identical():
             np.testing.assert_array_equal(out, first)
 
 
-def _band_check(got_full, spec, x, r0, r1, margin):
-    """Oracle on input rows [r0-margin, r1+margin) (full width); compares output rows
-    for input rows [r0, r1), which do not see the band's artificial edges."""
-    band = np.ascontiguousarray(x[:, :, r0 - margin:r1 + margin, :])
-    want = run_model(spec.model, band)
+def _window_oracle(model, x, r0, r1, c0, c1, margin, scale, round_fp16=True):
+    """Oracle output for input rows [r0, r1) and columns [c0, c1), run on the window
+    grown by `margin` pixels (at least one per 3x3 conv) and clipped to the image,
+    so the kept outputs never see the window's artificial edges."""
+    H, W = x.shape[2:]
+    a0, a1 = max(r0 - margin, 0), min(r1 + margin, H)
+    b0, b1 = max(c0 - margin, 0), min(c1 + margin, W)
+    win = np.ascontiguousarray(x[:, :, a0:a1, b0:b1])
+    y = run_model(model, win, round_fp16=round_fp16)
+    return y[:, :, (r0 - a0) * scale:(r1 - a0) * scale, (c0 - b0) * scale:(c1 - b0) * scale]
+
+
+def _band_check(got_full, spec, x, r0, r1, margin, c0=0, c1=None):
+    """Engine full-frame output for input rows [r0, r1) (and columns [c0, c1))
+    against the oracle on that window; returns (engine vs oracle, oracle floor)."""
+    c1 = x.shape[3] if c1 is None else c1
     s = spec.scale
-    want = want[:, :, margin * s:(margin + r1 - r0) * s, :]
-    got = got_full[:, :, r0 * s:r1 * s, :]
-    exact = run_model(spec.model, band, round_fp16=False)[:, :, margin * s:(margin + r1 - r0) * s, :]
+    want = _window_oracle(spec.model, x, r0, r1, c0, c1, margin, s)
+    exact = _window_oracle(spec.model, x, r0, r1, c0, c1, margin, s, round_fp16=False)
+    got = got_full[:, :, r0 * s:r1 * s, c0 * s:c1 * s]
     return _compare(got, want), _compare(want, exact)
 
 
@@ -119,7 +158,28 @@ def test_r8f64_full_1080p_band_parity():
     assert got.shape == (1, 1, 2160, 3840) and np.isfinite(got).all()
     s, floor = _band_check(got, spec, x, 520, 552, 18)
     print("r8f64 1080p band", s, "floor", floor)
-    assert s["rel_rms"] <= max(4 * floor["rel_rms"], 2e-3), (s, floor)
+    assert s["rel_rms"] <= max(FLOOR_RATIO * floor["rel_rms"], 2e-3), (s, floor)
+
+
+def test_r16f96_full_1080p_window_parity():
+    """R16F96 at full 1920x1080 (intermediates near 2e4, where fp16 overflow would
+    show first): finite everywhere, bit-stable across runs, and three windows (two
+    image corners and the middle) against the oracle with a 34-pixel margin (the
+    receptive field of 34 convs)."""
+    spec = models.r16f96(seed=0)
+    x = models.synthetic_input((1, 1, 1080, 1920), seed=1)
+    with Engine(0) as e:
+        got = e.build(spec).run(x)
+        again = e.run(x)
+    assert got.shape == (1, 1, 2160, 3840) and np.isfinite(got).all()
+    np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16))
+    got = got.astype(np.float32)
+    print("r16f96 1080p output range", float(got.min()), float(got.max()))
+    for r0, r1, c0, c1 in ((0, 24, 0, 96), (528, 552, 928, 1024), (1056, 1080, 1824, 1920)):
+        s, floor = _band_check(got, spec, x, r0, r1, 34, c0, c1)
+        print("r16f96 1080p window", (r0, r1, c0, c1), s, "floor", floor,
+              "ratio", s["rel_rms"] / floor["rel_rms"])
+        assert s["rel_rms"] <= max(FLOOR_RATIO * floor["rel_rms"], 2e-3), (s, floor)
 
 
 def test_r8f64_4k_batch2_full_size():
@@ -135,29 +195,74 @@ def test_r8f64_4k_batch2_full_size():
     np.testing.assert_array_equal(got[1:2], one)
     s, floor = _band_check(got[1:2].astype(np.float32), spec, x[1:2], 1000, 1016, 18)
     print("r8f64 4k band", s, "floor", floor)
-    assert s["rel_rms"] <= max(4 * floor["rel_rms"], 2e-3), (s, floor)
+    assert s["rel_rms"] <= max(FLOOR_RATIO * floor["rel_rms"], 2e-3), (s, floor)
 
 
-def test_shipped_model_on_real_image_meets_gate():
-    """The reference's shipped luma model on its own 256x256 test image (BT.601
-    luma): bounded [0,1] output, so the literal gate applies."""
+def _gray8(name):
+    """The reference's test image as its accuracy tool feeds it
+    (tests/tools/multires.py:84-92: cv2.imread(..., IMREAD_GRAYSCALE) / 255 as
+    fp16 NCHW): 8-bit BT.601 gray with OpenCV's fixed-point rounding,
+    (4899 R + 9617 G + 1868 B + 2^13) >> 14."""
     from pathlib import Path
 
     from PIL import Image
+    here = Path(__file__).resolve().parent / "golden"
+    rgb = np.asarray(Image.open(here / name).convert("RGB")).astype(np.int64)
+    g = (4899 * rgb[..., 0] + 9617 * rgb[..., 1] + 1868 * rgb[..., 2] + 8192) >> 14
+    x = np.clip(g.astype(np.float32) / 255.0, 0.0, 1.0)
+    return x[None, None].astype(np.float16)
+
+
+def _shipped_model():
+    from pathlib import Path
 
     from arthip_amd import onnx_proto as op
-    here = Path(__file__).resolve().parent / "golden"
-    rgb = np.asarray(Image.open(here / "test_256.png").convert("RGB"), np.float32) / 255.0
-    y = (rgb[..., 0] * 0.299 + rgb[..., 1] * 0.587 + rgb[..., 2] * 0.114)[None, None]
-    x = y.astype(np.float16)
-    model = op.load(here / "ArtCNN_R8F64_fp16.onnx")
+    return op.load(Path(__file__).resolve().parent / "golden" / "ArtCNN_R8F64_fp16.onnx")
+
+
+#: The shipped model against the oracle, held to the reference's own accuracy
+#: against ONNX Runtime CPU at 1920x1080 (0.00134; 0.00098 at 256;
+#: NOTES.md:78-79,294). The engine measures 0.0005-0.0006 in both oracle modes.
+SHIPPED_MAX_ABS = 1.34e-3
+
+
+def test_shipped_model_on_real_image_meets_gate():
+    """The reference's shipped luma model on its own 256x256 test image: bounded
+    [0,1] output, so the literal gate applies, and the reference's 1e-3 class."""
+    x = _gray8("test_256.png")
+    model = _shipped_model()
     with Engine(0) as e:
         got = e.build(model).run(x).astype(np.float32)
-    want = run_model(model, x)
-    s = _compare(got, want)
-    print("shipped luma 256x256", s)
-    assert got.shape == (1, 1, 512, 512)
-    assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
+    assert got.shape == (1, 1, 512, 512) and np.isfinite(got).all()
+    _literal_gate(got, model, x, "shipped luma 256x256", max_abs=SHIPPED_MAX_ABS)
+
+
+def test_shipped_model_full_1920_real_image():
+    """The product's real workload: the shipped luma model on the reference's
+    1920x1080 test photo at full size (the reference's accuracy gate,
+    NOTES.md:78-79). Finite, bit-stable across runs, and four windows (the two
+    corners, the middle, and a right-edge band) against the oracle in both modes,
+    with a 28-pixel margin (27 convs)."""
+    x = _gray8("test_1920.png")
+    assert x.shape == (1, 1, 1080, 1920)
+    model = _shipped_model()
+    with Engine(0) as e:
+        got = e.build(model).run(x)
+        again = e.run(x)
+    assert got.shape == (1, 1, 2160, 3840) and np.isfinite(got).all()
+    np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16))
+    got = got.astype(np.float32)
+    worst = {True: 0.0, False: 0.0}
+    for r0, r1, c0, c1 in ((0, 32, 0, 128), (524, 556, 896, 1024), (1048, 1080, 1792, 1920),
+                           (300, 332, 1792, 1920)):
+        part = got[:, :, 2 * r0:2 * r1, 2 * c0:2 * c1]
+        for mode in (True, False):
+            want = _window_oracle(model, x, r0, r1, c0, c1, 28, 2, round_fp16=mode)
+            s = _compare(part, want)
+            worst[mode] = max(worst[mode], s["max_abs"])
+            assert s["max_abs"] <= SHIPPED_MAX_ABS and s["psnr"] >= 50.0, ((r0, c0), mode, s)
+    print("shipped luma 1920x1080 max-abs vs oracle: fp16 storage %.5f, fp32 throughout %.5f "
+          "(reference vs ONNX Runtime CPU: 0.00134)" % (worst[True], worst[False]))
 
 
 @pytest.mark.parametrize("builder,hw", [(models.c4f32, (36, 52)), (models.r8f64, (24, 40)),
@@ -204,7 +309,10 @@ def test_tiny_frames(builder, hw):
     print(spec.name, hw, s, "floor", f)
     assert got.shape == want.shape
     assert np.isfinite(got).all()
-    assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
+    # 4 to 1000 outputs: the error ratio of so few samples is noisy (a 5x2 frame
+    # measures 3.5x its floor), so these frames get 4x and an absolute 4e-3; a
+    # wrong edge index costs an error of the order of the output itself.
+    assert s["rel_rms"] <= max(4 * f["rel_rms"], 4e-3), (s, f)
 
 
 @pytest.mark.parametrize("filters,out_ch,scale,clip,io32", [
@@ -236,7 +344,7 @@ def test_boundary_tail_convs(filters, out_ch, scale, clip, io32):
         print(filters, out_ch, scale, (h, w), s, "floor", f)
         assert got.shape == want.shape == (1, out_ch, h * scale, w * scale)
         assert np.isfinite(got).all()
-        assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
+        assert s["rel_rms"] <= max(FLOOR_RATIO * f["rel_rms"], 2e-3), (s, f)
         assert s["max_abs"] <= 2e-2, s
 
 
@@ -264,7 +372,7 @@ def test_head_reads_boundary_input(io32):
     want = run_model(spec.model, x)
     floor = run_model(spec.model, x, round_fp16=False)
     s, f = _compare(got.astype(np.float32), want), _compare(floor, want)
-    assert s["rel_rms"] <= max(4 * f["rel_rms"], 2e-3), (s, f)
+    assert s["rel_rms"] <= max(FLOOR_RATIO * f["rel_rms"], 2e-3), (s, f)
 
     # Same model with the graph input added to the tail's output: the input
     # is now also a residual operand.
@@ -280,7 +388,7 @@ def test_head_reads_boundary_input(io32):
     want2 = run_model(m, x)
     floor2 = run_model(m, x, round_fp16=False)
     s2, f2 = _compare(got2.astype(np.float32), want2), _compare(floor2, want2)
-    assert s2["rel_rms"] <= max(4 * f2["rel_rms"], 2e-3), (s2, f2)
+    assert s2["rel_rms"] <= max(FLOOR_RATIO * f2["rel_rms"], 2e-3), (s2, f2)
 
 
 @pytest.mark.parametrize("builder", [models.r8f64, models.shipped_like, models.r16f96],
@@ -303,6 +411,7 @@ def test_full_frame_equals_cropped_runs(builder):
     with Engine(0) as e:
         e.build(spec)
         full = e.run(x)
+        assert np.isfinite(full).all(), f"{spec.name}: non-finite output at 1080p"
         for r0, r1, c0, c1 in ((0, 48, 0, 64), (520, 552, 928, 1000), (H - 40, H, W - 64, W)):
             a0, a1 = max(r0 - m, 0), min(r1 + m, H)
             b0, b1 = max(c0 - m, 0), min(c1 + m, W)
