@@ -74,6 +74,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_engine_io_info", c_int, eng, i32p, i32p, i32p, i32p)
     sig("arthip_engine_run", c_int, eng, c_void, i64p, c_void, c_size, c_char, c_int)
     sig("arthip_engine_run_device", c_int, eng, c_void, i64p, c_void, c_void, c_char, c_int)
+    sig("arthip_engine_run_device_noalloc", c_int, eng, c_void, i64p, c_void, c_void, c_char,
+        c_int)
     sig("arthip_engine_describe", c_int, eng, c_char, c_int)
     sig("arthip_engine_set_profiling", c_int, eng, c_int)
     sig("arthip_engine_profile_read", c_int, eng, c_int, ctypes.POINTER(ctypes.c_double), i64p,
@@ -125,7 +127,8 @@ def _declare(lib: ctypes.CDLL) -> None:
 EXPORTED_SYMBOLS = (
     "arthip_engine_create", "arthip_engine_destroy", "arthip_engine_build_file",
     "arthip_engine_build_bytes", "arthip_engine_output_shape", "arthip_engine_io_info",
-    "arthip_engine_run", "arthip_engine_run_device", "arthip_engine_describe",
+    "arthip_engine_run", "arthip_engine_run_device", "arthip_engine_run_device_noalloc",
+    "arthip_engine_describe",
     "arthip_engine_set_profiling", "arthip_engine_profile_read", "arthip_engine_set_debug",
     "arthip_engine_get_debug",
     "engine_device_count", "engine_probe", "engine_run", "engine_alloc_failure_then_run",

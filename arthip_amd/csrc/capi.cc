@@ -183,6 +183,24 @@ int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64
   });
 }
 
+int arthip_engine_run_device_noalloc(arthip_engine* eng, const void* in_dev,
+                                     const int64_t in_nchw[4], void* out_dev, void* stream,
+                                     char* err, int errlen) {
+  return guard(ARTHIP_ERR_RUN, err, errlen, "", [&]() -> int {
+    if (eng == nullptr || in_nchw == nullptr)
+      return report("null engine or shape", ARTHIP_ERR_BUILD, err, errlen);
+    int64_t o[4];
+    if (!eng->eng->OutputShape(in_nchw, o))
+      return report("shape propagation failed", ARTHIP_ERR_BUILD, err, errlen);
+    std::string e;
+    if (!eng->eng->RunDeviceScratch(in_dev, in_nchw, out_dev, static_cast<hipStream_t>(stream),
+                                    e))
+      return report(e, ARTHIP_ERR_RUN, err, errlen);
+    copy_out("", err, errlen);
+    return ARTHIP_OK;
+  });
+}
+
 int arthip_engine_describe(const arthip_engine* eng, char* buf, int buflen) {
   return guard(ARTHIP_ERR_BUILD, nullptr, 0, "", [&]() -> int {
     if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);

@@ -119,6 +119,13 @@ bool Engine::Init(std::string& error) {
     error = HipErr("hipStreamCreate", e);
     return false;
   }
+  // Set-up of the no-allocation entry point's scratch on this device (its
+  // address is resolved once per device, here with the device current), so
+  // that entry point's own calls load and resolve nothing. A failure is
+  // reported by that entry point.
+  void* scratch = nullptr;
+  std::string ignored;
+  (void)scratch_address(device_, &scratch, ignored);
   return true;
 }
 
@@ -210,27 +217,31 @@ size_t Engine::OutputBytesUnlocked(const int64_t in[4]) const {
   return static_cast<size_t>(o[0] * o[1] * o[2] * o[3]) * (graph_.output_fp32 ? 4 : 2);
 }
 
+void Engine::ClearPlan(Plan& p) {
+  const bool scratch = p.scratch;
+  p = Plan{};
+  p.scratch = scratch;
+}
+
 void Engine::FreePlan() {
   prof_acc_.clear();
-  const bool any = !bufs_.empty() || in_stage_dev_ || out_stage_dev_ || in_pinned_ || out_pinned_;
+  const bool any =
+      !plan_.bufs.empty() || in_stage_dev_ || out_stage_dev_ || in_pinned_ || out_pinned_;
   if (any) hipSetDevice(device_);  // frees need the owning device current on this thread
   DrainPrevious();  // the last run may still read or write these buffers
-  for (auto& b : bufs_)
+  for (auto& b : plan_.bufs)
     if (b.ptr) hipFree(b.ptr);
-  bufs_.clear();
-  buf_names_.clear();
-  steps_.clear();
   if (in_stage_dev_) hipFree(in_stage_dev_);
   if (out_stage_dev_) hipFree(out_stage_dev_);
   if (in_pinned_) hipHostFree(in_pinned_);
   if (out_pinned_) hipHostFree(out_pinned_);
   in_stage_dev_ = out_stage_dev_ = in_pinned_ = out_pinned_ = nullptr;
-  in_bytes_ = out_bytes_ = 0;
-  planned_ = false;
+  ClearPlan(plan_);
 }
 
 void Engine::FreeAll() {
   FreePlan();
+  ClearPlan(scratch_plan_);
   if (!wbufs_.empty()) hipSetDevice(device_);
   DrainPrevious();
   for (auto& b : wbufs_)
@@ -300,13 +311,17 @@ bool Engine::EnsureWeights(std::string& error) {
   return true;
 }
 
-bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
-  if (planned_ && std::equal(in, in + 4, plan_in_)) return true;
+bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* scratch,
+                        size_t cap) {
+  if (p.planned && std::equal(in, in + 4, p.in)) return true;
   if (!built_) {
     error = "engine has no model (build first)";
     return false;
   }
-  FreePlan();
+  if (p.scratch)
+    ClearPlan(p);  // nothing of a scratch plan is allocated
+  else
+    FreePlan();
   std::unordered_map<std::string, Shape> shapes;
   if (!PropagateShapes(graph_, in, shapes)) {
     error = "shape propagation failed (unsupported convolution geometry, channel mismatch, "
@@ -364,19 +379,30 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
     DevBuf b;
     b.bytes = PaddedBytes(s);
     b.geo = s;
-    const hipError_t e = hipMalloc(&b.ptr, b.bytes);
-    if (e != hipSuccess) {
-      error = "hipMalloc of " + std::to_string(b.bytes) + " bytes for tensor '" + name +
-              "' failed: " + hipGetErrorString(e);
-      return false;
+    if (p.scratch) {
+      // Laid out in the scratch array at 256-byte alignment; whether the plan
+      // fits is checked once the whole layout is known.
+      const size_t off = (p.act_bytes + 255) & ~static_cast<size_t>(255);
+      b.ptr = off + b.bytes <= cap ? static_cast<char*>(scratch) + off : nullptr;
+      p.act_bytes = off + b.bytes;
+    } else {
+      const hipError_t e = hipMalloc(&b.ptr, b.bytes);
+      if (e != hipSuccess) {
+        error = "hipMalloc of " + std::to_string(b.bytes) + " bytes for tensor '" + name +
+                "' failed: " + hipGetErrorString(e);
+        return false;
+      }
+      p.act_bytes += b.bytes;
     }
-    bufs_.push_back(b);
-    buf_names_.push_back(name);
-    const int idx = static_cast<int>(bufs_.size()) - 1;
-    const hipError_t z = hipMemsetAsync(b.ptr, 0, b.bytes, stream_);  // zero border
-    if (z != hipSuccess) {
-      error = HipErr("hipMemsetAsync of an activation buffer", z);
-      return false;
+    p.bufs.push_back(b);
+    p.buf_names.push_back(name);
+    const int idx = static_cast<int>(p.bufs.size()) - 1;
+    if (!p.scratch) {
+      const hipError_t z = hipMemsetAsync(b.ptr, 0, b.bytes, stream_);  // zero border
+      if (z != hipSuccess) {
+        error = HipErr("hipMemsetAsync of an activation buffer", z);
+        return false;
+      }
     }
     slots.push_back(Slot{idx, last_use.count(name) ? last_use[name] : producer, s});
     tbuf[name] = idx;
@@ -384,7 +410,10 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
   };
 
   auto fail = [&]() {
-    FreePlan();
+    if (p.scratch)
+      ClearPlan(p);
+    else
+      FreePlan();
     return false;
   };
 
@@ -421,7 +450,7 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
     st.out = tbuf[graph_.input_name];
     st.N = (int32_t)sin.n; st.H = (int32_t)sin.h; st.W = (int32_t)sin.w; st.C = (int32_t)sin.c;
     st.fp32 = graph_.input_fp32 ? 1 : 0;
-    steps_.push_back(st);
+    p.steps.push_back(st);
   }
 
   const int out_kind_boundary = graph_.output_fp32 ? kOutNchwF32 : kOutNchwF16;
@@ -494,7 +523,7 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
         st.hi = op.clip_hi;
         break;
     }
-    steps_.push_back(st);
+    p.steps.push_back(st);
   }
 
   if (!direct_out) {
@@ -505,37 +534,51 @@ bool Engine::EnsurePlan(const int64_t in[4], std::string& error) {
     st.out = kBoundaryOut;
     st.N = (int32_t)so.n; st.H = (int32_t)so.h; st.W = (int32_t)so.w; st.C = (int32_t)so.c;
     st.fp32 = graph_.output_fp32 ? 1 : 0;
-    steps_.push_back(st);
+    p.steps.push_back(st);
   }
 
-  in_bytes_ = static_cast<size_t>(in[0] * in[1] * in[2] * in[3]) * (graph_.input_fp32 ? 4 : 2);
-  out_bytes_ = OutputBytesUnlocked(in);
-  hipError_t e = hipStreamSynchronize(stream_);  // buffer zeroing done
-  if (e != hipSuccess) {
-    error = HipErr("hipStreamSynchronize after plan setup", e);
-    return fail();
+  p.in_bytes = static_cast<size_t>(in[0] * in[1] * in[2] * in[3]) * (graph_.input_fp32 ? 4 : 2);
+  p.out_bytes = OutputBytesUnlocked(in);
+  if (p.scratch) {
+    if (p.act_bytes > cap) {
+      error = "the activations of a " + std::to_string(in[0]) + "x" + std::to_string(in[1]) +
+              "x" + std::to_string(in[2]) + "x" + std::to_string(in[3]) + " input need " +
+              std::to_string(p.act_bytes) + " bytes; the no-allocation scratch holds " +
+              std::to_string(cap) + " bytes (use arthip_engine_run_device for larger inputs)";
+      return fail();
+    }
+  } else {
+    const hipError_t e = hipStreamSynchronize(stream_);  // buffer zeroing done
+    if (e != hipSuccess) {
+      error = HipErr("hipStreamSynchronize after plan setup", e);
+      return fail();
+    }
   }
-  std::copy(in, in + 4, plan_in_);
-  planned_ = true;
+  std::copy(in, in + 4, p.in);
+  p.planned = true;
   return true;
 }
 
-bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::string& error) {
+bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream_t s,
+                     std::string& error) {
   auto ptr = [&](int idx) -> void* {
     if (idx == kBoundaryIn) return const_cast<void*>(in_dev);
     if (idx == kBoundaryOut) return out_dev;
     if (idx < 0) return nullptr;
-    return bufs_[idx].ptr;
+    return p.bufs[idx].ptr;
   };
   auto bytes_of = [&](int idx) -> size_t {
-    if (idx == kBoundaryIn) return in_bytes_;
-    if (idx == kBoundaryOut) return out_bytes_;
+    if (idx == kBoundaryIn) return p.in_bytes;
+    if (idx == kBoundaryOut) return p.out_bytes;
     if (idx < 0) return 0;
-    return bufs_[idx].bytes;
+    return p.bufs[idx].bytes;
   };
-  if (profiling_ && prof_acc_.size() != steps_.size()) {
-    prof_acc_.assign(steps_.size(), StepProfile{});
-    for (size_t i = 0; i < steps_.size(); ++i) prof_acc_[i].name = StepName(steps_[i]);
+  // Profiling events and dumps create events and host buffers: runs on a
+  // scratch plan do neither.
+  const bool profiling = profiling_ && !p.scratch;
+  if (profiling && prof_acc_.size() != p.steps.size()) {
+    prof_acc_.assign(p.steps.size(), StepProfile{});
+    for (size_t i = 0; i < p.steps.size(); ++i) prof_acc_[i].name = StepName(p.steps[i]);
   }
   if (!WaitPrevious(s, error)) return false;
   // From here on the run's work is on s: later runs order after it even when
@@ -550,11 +593,24 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
     return ok;
   };
 
+  // A scratch plan's buffers hold whatever the last user of the scratch array
+  // left: clear their borders, the zero padding every conv reads, with a
+  // kernel (no memset node for callers that capture the stream).
+  if (p.scratch) {
+    for (const DevBuf& b : p.bufs) {
+      const hipError_t e = launch_zero_border(b.ptr, (int32_t)b.geo.n, (int32_t)b.geo.h,
+                                              (int32_t)b.geo.w, (int32_t)b.geo.c, s);
+      if (e != hipSuccess) {
+        error = HipErr("scratch border clear", e);
+        return finish(false);
+      }
+    }
+  }
   // VSHIP_POISON: every activation interior becomes fp16 NaN (0x7E7E), the
   // reference's poison pattern; the zero border stays. A launch that reads a
   // tensor no earlier launch of this run wrote then yields NaN.
   if (debug_ & kDebugPoison) {
-    for (const DevBuf& b : bufs_) {
+    for (const DevBuf& b : p.bufs) {
       const hipError_t e = launch_poison(b.ptr, (int32_t)b.geo.n, (int32_t)b.geo.h,
                                          (int32_t)b.geo.w, (int32_t)b.geo.c, 0x7E7E, s);
       if (e != hipSuccess) {
@@ -565,14 +621,15 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
   }
   // VSHIP_DUMP: each launch's inputs and output as raw files, for the first
   // two runs of the engine. Activations are padded NHWC fp16 buffers.
-  const bool dump = (debug_ & kDebugDump) != 0 && !dump_dir_.empty() && dump_runs_ < 2;
+  const bool dump =
+      !p.scratch && (debug_ & kDebugDump) != 0 && !dump_dir_.empty() && dump_runs_ < 2;
   const uint64_t dump_run = dump ? ++dump_runs_ : 0;
 
-  for (size_t i = 0; i < steps_.size(); ++i) {
-    const Step& st = steps_[i];
+  for (size_t i = 0; i < p.steps.size(); ++i) {
+    const Step& st = p.steps[i];
     hipError_t e = hipSuccess;
     EventPair ev{static_cast<int>(i), nullptr, nullptr};
-    if (profiling_) {
+    if (profiling) {
       ev.start = TakeEvent();
       ev.stop = TakeEvent();
       if (ev.start == nullptr || ev.stop == nullptr || hipEventRecord(ev.start, s) != hipSuccess) {
@@ -654,7 +711,7 @@ bool Engine::Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::stri
               hipGetErrorString(e);
       return finish(false);
     }
-    if (profiling_) {
+    if (profiling) {
       if (hipEventRecord(ev.stop, s) != hipSuccess) {
         error = "HIP event record for profiling failed";
         return finish(false);
@@ -773,35 +830,36 @@ bool Engine::Run(const void* in_host, const int64_t in[4], void* out_host, size_
   std::lock_guard<std::mutex> lock(mu_);
   (void)hipGetLastError();  // a stale error from an earlier failed call is not this run's
   if (!Init(error)) return false;
-  if (!EnsurePlan(in, error)) return false;
+  if (!EnsurePlan(plan_, in, error)) return false;
+  const size_t in_bytes = plan_.in_bytes, out_bytes = plan_.out_bytes;
   if (in_host == nullptr || out_host == nullptr) {
     error = "null host buffer";
     return false;
   }
-  if (out_cap < out_bytes_) {
+  if (out_cap < out_bytes) {
     error = "output buffer too small (" + std::to_string(out_cap) + " bytes, need " +
-            std::to_string(out_bytes_) + ")";
+            std::to_string(out_bytes) + ")";
     return false;
   }
   hipError_t e;
   if (in_stage_dev_ == nullptr) {
-    if ((e = hipMalloc(&in_stage_dev_, in_bytes_)) != hipSuccess ||
-        (e = hipMalloc(&out_stage_dev_, out_bytes_)) != hipSuccess ||
-        (e = hipHostMalloc(&in_pinned_, in_bytes_, hipHostMallocDefault)) != hipSuccess ||
-        (e = hipHostMalloc(&out_pinned_, out_bytes_, hipHostMallocDefault)) != hipSuccess) {
+    if ((e = hipMalloc(&in_stage_dev_, in_bytes)) != hipSuccess ||
+        (e = hipMalloc(&out_stage_dev_, out_bytes)) != hipSuccess ||
+        (e = hipHostMalloc(&in_pinned_, in_bytes, hipHostMallocDefault)) != hipSuccess ||
+        (e = hipHostMalloc(&out_pinned_, out_bytes, hipHostMallocDefault)) != hipSuccess) {
       error = "hipMalloc of IO staging failed: " + std::string(hipGetErrorString(e));
       FreePlan();
       return false;
     }
   }
-  std::memcpy(in_pinned_, in_host, in_bytes_);
-  if ((e = hipMemcpyAsync(in_stage_dev_, in_pinned_, in_bytes_, hipMemcpyHostToDevice,
+  std::memcpy(in_pinned_, in_host, in_bytes);
+  if ((e = hipMemcpyAsync(in_stage_dev_, in_pinned_, in_bytes, hipMemcpyHostToDevice,
                           stream_)) != hipSuccess) {
     error = HipErr("HIP input upload", e);
     return false;
   }
-  if (!Enqueue(in_stage_dev_, out_stage_dev_, stream_, error)) return false;
-  if ((e = hipMemcpyAsync(out_pinned_, out_stage_dev_, out_bytes_, hipMemcpyDeviceToHost,
+  if (!Enqueue(plan_, in_stage_dev_, out_stage_dev_, stream_, error)) return false;
+  if ((e = hipMemcpyAsync(out_pinned_, out_stage_dev_, out_bytes, hipMemcpyDeviceToHost,
                           stream_)) != hipSuccess) {
     error = HipErr("HIP output download", e);
     return false;
@@ -810,7 +868,7 @@ bool Engine::Run(const void* in_host, const int64_t in[4], void* out_host, size_
     error = HipErr("HIP stream synchronize", e);
     return false;
   }
-  std::memcpy(out_host, out_pinned_, out_bytes_);
+  std::memcpy(out_host, out_pinned_, out_bytes);
   return true;
 }
 
@@ -819,12 +877,34 @@ bool Engine::RunDevice(const void* in_dev, const int64_t in[4], void* out_dev,
   std::lock_guard<std::mutex> lock(mu_);
   (void)hipGetLastError();
   if (!Init(error)) return false;
-  if (!EnsurePlan(in, error)) return false;
+  if (!EnsurePlan(plan_, in, error)) return false;
   if (in_dev == nullptr || out_dev == nullptr) {
     error = "null device buffer";
     return false;
   }
-  return Enqueue(in_dev, out_dev, stream ? stream : stream_, error);
+  return Enqueue(plan_, in_dev, out_dev, stream ? stream : stream_, error);
+}
+
+bool Engine::RunDeviceScratch(const void* in_dev, const int64_t in[4], void* out_dev,
+                              hipStream_t stream, std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  (void)hipGetLastError();
+  if (stream_ == nullptr || run_done_ == nullptr || !weights_ready_) {
+    error = "the engine is not set up on its device yet: one run (arthip_engine_run or "
+            "arthip_engine_run_device, any input size) creates its stream and uploads its "
+            "weights; the no-allocation entry point does neither";
+    return false;
+  }
+  if (!SetDevice(error)) return false;
+  void* scratch = nullptr;
+  if (!scratch_address(device_, &scratch, error)) return false;
+  scratch_plan_.scratch = true;
+  if (!EnsurePlan(scratch_plan_, in, error, scratch, kNoAllocScratchBytes)) return false;
+  if (in_dev == nullptr || out_dev == nullptr) {
+    error = "null device buffer";
+    return false;
+  }
+  return Enqueue(scratch_plan_, in_dev, out_dev, stream ? stream : stream_, error);
 }
 
 std::string Engine::Describe() const {
@@ -846,13 +926,11 @@ std::string Engine::Describe() const {
     if (op.clip) os << " +clip[" << op.clip_lo << "," << op.clip_hi << "]";
     os << " : " << op.in0 << (op.in1.empty() ? "" : ", " + op.in1) << " -> " << op.out << "\n";
   }
-  if (planned_) {
-    os << "plan for [" << plan_in_[0] << "," << plan_in_[1] << "," << plan_in_[2] << ","
-       << plan_in_[3] << "]: " << steps_.size() << " launches, " << bufs_.size()
-       << " activation buffers:";
-    size_t total = 0;
-    for (const auto& b : bufs_) total += b.bytes;
-    os << " " << total << " bytes\n";
+  for (const Plan* p : {&plan_, &scratch_plan_}) {
+    if (!p->planned) continue;
+    os << (p->scratch ? "scratch plan" : "plan") << " for [" << p->in[0] << "," << p->in[1]
+       << "," << p->in[2] << "," << p->in[3] << "]: " << p->steps.size() << " launches, "
+       << p->bufs.size() << " activation buffers: " << p->act_bytes << " bytes\n";
   }
   return os.str();
 }

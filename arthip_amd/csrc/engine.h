@@ -62,6 +62,18 @@ struct Step {
   int32_t in_kind = 0;  // direct conv reading the boundary input: 1 fp16, 2 fp32
 };
 
+// One input shape's launch list and activation buffers.
+struct Plan {
+  bool planned = false;
+  bool scratch = false;  // activations live in the no-allocation scratch array
+  int64_t in[4] = {0, 0, 0, 0};
+  std::vector<DevBuf> bufs;
+  std::vector<Step> steps;
+  std::vector<std::string> buf_names;
+  size_t in_bytes = 0, out_bytes = 0;
+  size_t act_bytes = 0;  // activation bytes (for a scratch plan: the extent used)
+};
+
 class Engine {
  public:
   explicit Engine(int device_id);
@@ -99,6 +111,15 @@ class Engine {
   bool RunDevice(const void* in_dev, const int64_t in_nchw[4], void* out_dev, hipStream_t stream,
                  std::string& error);
 
+  // RunDevice without any device allocation: the activations go to `scratch`
+  // (scratch_cap bytes of device memory that the caller owns for the call) in
+  // a plan of their own; borders are cleared by a kernel each run. Needs the
+  // engine initialized and its weights resident (any earlier Run / RunDevice
+  // does both). Not profiled and not dumped.
+  bool RunDeviceScratch(const void* in_dev, const int64_t in_nchw[4], void* out_dev,
+                        hipStream_t stream, std::string& error);
+  int Device() const { return device_; }
+
   // Diagnostics (DebugFlag bits); dump_dir is used with kDebugDump.
   void SetDebug(int flags, const std::string& dump_dir);
   int DebugFlags() const;
@@ -123,10 +144,16 @@ class Engine {
   bool SetDevice(std::string& error) const;
   bool OutputShapeUnlocked(const int64_t in_nchw[4], int64_t out_nchw[4]) const;
   size_t OutputBytesUnlocked(const int64_t in_nchw[4]) const;
-  bool EnsurePlan(const int64_t in_nchw[4], std::string& error);
+  // Builds p for this input shape (cached per shape). With p.scratch the
+  // activations are laid out from `scratch` (cap bytes) and nothing is
+  // allocated; otherwise each buffer is a zeroed hipMalloc.
+  bool EnsurePlan(Plan& p, const int64_t in_nchw[4], std::string& error, void* scratch = nullptr,
+                  size_t cap = 0);
   bool EnsureWeights(std::string& error);
-  bool Enqueue(const void* in_dev, void* out_dev, hipStream_t s, std::string& error);
-  void FreePlan();
+  bool Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream_t s,
+               std::string& error);
+  static void ClearPlan(Plan& p);
+  void FreePlan();  // the allocated plan and the host-path staging
   void FreeAll();
 
   int device_;
@@ -149,13 +176,10 @@ class Engine {
   std::vector<DevBuf> wbufs_;
   std::unordered_map<int, int> op_wbuf_, op_bbuf_;  // op index -> wbufs_ index
 
-  // Current plan.
-  bool planned_ = false;
-  int64_t plan_in_[4] = {0, 0, 0, 0};
-  std::vector<DevBuf> bufs_;
-  std::vector<Step> steps_;
-  std::vector<std::string> buf_names_;
-  size_t in_bytes_ = 0, out_bytes_ = 0;
+  // Current plans: allocated activations (Run, RunDevice) and activations in
+  // the scratch array (RunDeviceScratch).
+  Plan plan_;
+  Plan scratch_plan_;
   // Host Run path: device copies of the boundary tensors and pinned staging.
   void* in_stage_dev_ = nullptr;
   void* out_stage_dev_ = nullptr;

@@ -2253,6 +2253,36 @@ __global__ void __launch_bounds__(256) poison_interior(uint16_t* buf, int32_t N,
   }
 }
 
+// Zero fill of everything but the interior of a padded NHWC fp16 buffer: the
+// Hp - H rows above and below the image (full width), then, on each image
+// row, the Wp - W columns left and right of it. One thread per element.
+__global__ void __launch_bounds__(256) zero_border(uint16_t* buf, int32_t N, int32_t H, int32_t W,
+                                                   int32_t C, int32_t Hp, int32_t Wp) {
+  const int64_t rows_px = (int64_t)(Hp - H) * Wp;  // top row + rows below the image
+  const int64_t side = Wp - W;                      // left column + columns right of it
+  const int64_t per_img = rows_px + (int64_t)H * side;
+  const int64_t total = (int64_t)N * per_img * C;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % C);
+    const int64_t r = i / C;
+    const int64_t n = r / per_img;
+    const int64_t k = r % per_img;
+    int64_t row, col;
+    if (k < rows_px) {
+      const int64_t q = k / Wp;
+      row = q == 0 ? 0 : H + q;
+      col = k % Wp;
+    } else {
+      const int64_t k2 = k - rows_px;
+      row = 1 + k2 / side;
+      const int64_t j = k2 % side;
+      col = j == 0 ? 0 : W + j;
+    }
+    buf[((n * Hp + row) * Wp + col) * C + c] = 0;
+  }
+}
+
 // VapourSynth plane samples <-> NCHW boundary elements, one element per
 // thread step (src/vapoursynth/vs_hip.cpp:175-225 packs on the host,
 // 347-369 unpacks integer output):
@@ -2727,6 +2757,17 @@ hipError_t launch_poison(void* buf, int32_t N, int32_t H, int32_t W, int32_t C, 
   hipLaunchKernelGGL(poison_interior, dim3(grid_for(total, 256)), dim3(256), 0, s,
                      static_cast<uint16_t*>(buf), N, H, W, C, (int32_t)padded_rows(H),
                      (int32_t)padded_cols(W), (uint32_t)pattern);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_border(void* buf, int32_t N, int32_t H, int32_t W, int32_t C,
+                              hipStream_t s) {
+  if (buf == nullptr || N < 0 || H < 0 || W < 0 || C < 0) return hipErrorInvalidValue;
+  const int64_t Hp = padded_rows(H), Wp = padded_cols(W);
+  const int64_t total = (int64_t)N * ((Hp - H) * Wp + (int64_t)H * (Wp - W)) * C;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_border, dim3(grid_for(total, 256)), dim3(256), 0, s,
+                     static_cast<uint16_t*>(buf), N, H, W, C, (int32_t)Hp, (int32_t)Wp);
   return hipGetLastError();
 }
 

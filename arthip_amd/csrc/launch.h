@@ -4,6 +4,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
+#include <string>
+
 #include "conv_args.h"
 
 namespace arthip {
@@ -23,5 +26,17 @@ hipError_t launch_plane_convert(PlaneArgs a, hipStream_t s);
 // tensor with `pattern` (diagnostics); the border keeps its zeros.
 hipError_t launch_poison(void* buf, int32_t N, int32_t H, int32_t W, int32_t C, uint16_t pattern,
                          hipStream_t s);
+// Zeroes everything of a padded NHWC fp16 buffer holding an N x H x W x C
+// tensor except the interior: the border rows and columns (and the extra
+// row / column of an odd H / W) that the convs read as zero padding.
+hipError_t launch_zero_border(void* buf, int32_t N, int32_t H, int32_t W, int32_t C,
+                              hipStream_t s);
+
+// The no-allocation entry point's scratch: a file-scope device array of this
+// many bytes, one copy on every GPU the library's code is loaded on, held until
+// the process ends. scratch_address gives its address on `device`, which must
+// be the calling thread's current device (resolved once per device).
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(256) << 20;
+bool scratch_address(int device, void** ptr, std::string& error);
 
 }  // namespace arthip

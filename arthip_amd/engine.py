@@ -248,6 +248,20 @@ class Engine:
             raise EngineError(_msg(e, f"run_device failed (rc={rc})"))
 
 
+    def run_device_noalloc(self, x, out, stream=None) -> None:
+        """run_device with the activations in the library's scratch array: no
+        device allocation (for callers that cannot allocate). Needs one earlier
+        run or run_device on this engine; inputs whose activations exceed the
+        scratch are refused."""
+        e = _err()
+        s = ctypes.c_void_p(stream) if stream is not None else None
+        rc = self._lib.arthip_engine_run_device_noalloc(
+            self._h, ctypes.c_void_p(x.data_ptr()), _shape(tuple(x.shape)),
+            ctypes.c_void_p(out.data_ptr()), s, e, _ERR_LEN)
+        if rc != 0:
+            raise EngineError(_msg(e, f"run_device_noalloc failed (rc={rc})"))
+
+
 # ---------------------------------------------------------------------------
 # Reference-style test driver
 # ---------------------------------------------------------------------------

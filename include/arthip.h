@@ -80,6 +80,32 @@ int arthip_engine_run(arthip_engine* eng, const void* in_host, const int64_t in_
 int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64_t in_nchw[4],
                              void* out_dev, void* stream, char* err, int errlen);
 
+/* No counterpart in the reference: run_device for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results as
+ * arthip_engine_run_device, but the intermediate activations live in the
+ * library's scratch array, a file-scope device array of
+ * ARTHIP_NOALLOC_SCRATCH_BYTES (256 MiB) that every GPU the library runs on
+ * holds until the process ends; this call makes no hipMalloc, hipFree or other
+ * allocating call.
+ * - An input whose activations need more than the scratch holds is refused
+ *   (return 2, with the bytes needed), before anything is enqueued. R8F64
+ *   fits up to 960x540; R8F64 at 1920x1080 needs about 1.06 GB and must use
+ *   run_device.
+ * - The handle must have run once through arthip_engine_run or
+ *   arthip_engine_run_device (any input size, e.g. a 2x2 warm-up): that run
+ *   creates the engine's stream and uploads its weights. Otherwise return 2.
+ * - Every call on one GPU shares that GPU's scratch, which keeps the last
+ *   call's contents (each call clears the zero padding it needs). Calls on one
+ *   handle are ordered on the GPU like run_device; calls on different handles
+ *   that overlap in time on one GPU race on the scratch and corrupt each
+ *   other's results: callers must serialize them.
+ * - Not profiled and not dumped (those create events and host buffers). */
+#define ARTHIP_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+int arthip_engine_run_device_noalloc(arthip_engine* eng, const void* in_dev,
+                                     const int64_t in_nchw[4], void* out_dev, void* stream,
+                                     char* err, int errlen);
+
 /* Human-readable plan of the last built shape (op list, fusions, buffers). */
 int arthip_engine_describe(const arthip_engine* eng, char* buf, int buflen);
 
