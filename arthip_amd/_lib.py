@@ -114,6 +114,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_conv3x3_pack", c_int, u16p, u16p, c_int, c_int, u16p, c_size, f32p, c_size)
     sig("arthip_conv3x3_f16_nhwc", c_int, c_void, c_void, c_void, c_int, c_void, c_void, c_void,
         c_int, c_int, c_int, c_int, c_int, c_void)
+    sig("arthip_conv3x3_block_f16_nhwc", c_int, c_void, c_void, c_void, c_int, c_void, c_void,
+        c_void, c_void, c_void, c_int, c_int, c_int, c_int, c_void)
     sig("arthip_conv3x3_limits", c_int, i32p, i32p)
     sig("arthip_padded_dims", c_int, c_int, c_int, i32p, i32p)
     sig("arthip_f32_to_f16", ctypes.c_uint16, ctypes.c_float)
@@ -136,7 +138,7 @@ EXPORTED_SYMBOLS = (
     "arthip_vs_model_create", "arthip_vs_model_get_frame", "arthip_vs_model_destroy",
     "arthip_vs_version", "arthip_vs_device_properties",
     "arthip_conv3x3_packed_halfs", "arthip_conv3x3_bias_len", "arthip_conv3x3_pack",
-    "arthip_conv3x3_f16_nhwc", "arthip_conv3x3_limits", "arthip_padded_dims", "arthip_f32_to_f16",
+    "arthip_conv3x3_f16_nhwc", "arthip_conv3x3_block_f16_nhwc", "arthip_conv3x3_limits", "arthip_padded_dims", "arthip_f32_to_f16",
     "arthip_f16_to_f32", "arthip_f32_to_f16_no_subnormals", "arthip_last_error", "arthip_version",
 )
 

@@ -218,7 +218,8 @@ int arthip_engine_set_profiling(arthip_engine* eng, int on) {
 int arthip_engine_set_debug(arthip_engine* eng, int flags, const char* dump_dir) {
   return guard(ARTHIP_ERR_BUILD, nullptr, 0, "", [&]() -> int {
     if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);
-    if ((flags & ~(ARTHIP_DEBUG_POISON | ARTHIP_DEBUG_SYNC_EACH | ARTHIP_DEBUG_DUMP)) != 0)
+    if ((flags & ~(ARTHIP_DEBUG_POISON | ARTHIP_DEBUG_SYNC_EACH | ARTHIP_DEBUG_DUMP |
+                   ARTHIP_DEBUG_UNFUSED)) != 0)
       return fail("unknown debug flag", ARTHIP_ERR_BUILD);
     if ((flags & ARTHIP_DEBUG_DUMP) && (dump_dir == nullptr || *dump_dir == '\0'))
       return fail("dump requested without a directory", ARTHIP_ERR_BUILD);
@@ -658,6 +659,44 @@ int arthip_conv3x3_f16_nhwc(const void* in, const void* packed, const float* bia
   }
   if (err != hipSuccess)
     return fail(std::string("conv3x3 launch failed: ") + hipGetErrorString(err), ARTHIP_ERR_RUN);
+  return ARTHIP_OK;
+}
+
+int arthip_conv3x3_block_f16_nhwc(const void* in, const void* packed1, const float* bias1,
+                                  int act1, const void* packed2, const float* bias2,
+                                  const void* skip0, const void* skip1, void* out, int N, int H,
+                                  int W, int C, void* stream) {
+  if (in == nullptr || packed1 == nullptr || bias1 == nullptr || packed2 == nullptr ||
+      bias2 == nullptr || out == nullptr)
+    return fail("arthip_conv3x3_block_f16_nhwc: null buffer", ARTHIP_ERR_BUILD);
+  if (skip0 == nullptr && skip1 != nullptr)
+    return fail("arthip_conv3x3_block_f16_nhwc: skip1 without skip0", ARTHIP_ERR_BUILD);
+  if (out == in || (skip0 != nullptr && out == skip0) || (skip1 != nullptr && out == skip1))
+    return fail("arthip_conv3x3_block_f16_nhwc: out must not alias an input", ARTHIP_ERR_BUILD);
+  if (act1 < 0 || act1 > 2)
+    return fail("arthip_conv3x3_block_f16_nhwc: unknown activation", ARTHIP_ERR_BUILD);
+  if (!arthip::block_eligible(C, C, act1, arthip::kActNone, N, H, W))
+    return fail("arthip_conv3x3_block_f16_nhwc: the fused block needs C = 64, N, H, W >= 1 and "
+                "a padded image below 2 GiB",
+                ARTHIP_ERR_BUILD);
+  arthip::BlockArgs a{};
+  a.in = static_cast<const uint16_t*>(in);
+  a.u1 = static_cast<const uint16_t*>(packed1);
+  a.bias1 = bias1;
+  a.u2 = static_cast<const uint16_t*>(packed2);
+  a.bias2 = bias2;
+  a.skip0 = static_cast<const uint16_t*>(skip0);
+  a.skip1 = static_cast<const uint16_t*>(skip1);
+  a.out = static_cast<uint16_t*>(out);
+  a.N = N;
+  a.H = H;
+  a.W = W;
+  a.act1 = act1;
+  a.act2 = arthip::kActNone;
+  const hipError_t err = arthip::launch_block(a, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess)
+    return fail(std::string("conv3x3 block launch failed: ") + hipGetErrorString(err),
+                ARTHIP_ERR_RUN);
   return ARTHIP_OK;
 }
 

@@ -84,6 +84,27 @@ struct StripArgs {
   FastDiv fd_tiles_h, fd_strips;
 };
 
+// Fused residual block of two 64 -> 64 convs (winograd_block in kernels.hip):
+// out = act2(conv2(act1(conv1(in) + bias1)) + bias2) + skip0 + skip1, every
+// tensor padded NHWC fp16 with the input's geometry. Work items are 1 output
+// tile row x 15 tiles (a 30-pixel strip), ordered (n, strip, tile row) with the
+// tile row fastest.
+struct BlockArgs {
+  const uint16_t* in;
+  const uint16_t* u1;  // packed transformed filters of conv1 (winograd_pack)
+  const float* bias1;  // [64] fp32
+  const uint16_t* u2;
+  const float* bias2;
+  const uint16_t* skip0;  // or null
+  const uint16_t* skip1;  // or null (only with skip0)
+  uint16_t* out;
+  int32_t N, H, W, Hp, Wp;
+  int32_t act1, act2;
+  int32_t tiles_h, n_strips;
+  int32_t n_items;  // N * n_strips * tiles_h
+  FastDiv fd_tiles_h, fd_strips;
+};
+
 // Direct 3x3 conv on MFMA for M <= 16 outputs written to the boundary NCHW
 // layout (conv3x3_narrow in kernels.hip). Work items are 1 output row x 64
 // pixels, ordered (n, 64-pixel segment, row) with the row fastest.

@@ -57,7 +57,12 @@ Engine::~Engine() {
 
 void Engine::SetDebug(int flags, const std::string& dump_dir) {
   std::lock_guard<std::mutex> lock(mu_);
-  debug_ = flags & (kDebugPoison | kDebugSyncEach | kDebugDump);
+  flags &= kDebugPoison | kDebugSyncEach | kDebugDump | kDebugUnfused;
+  if ((flags ^ debug_) & kDebugUnfused) {  // the plans depend on it
+    FreePlan();
+    ClearPlan(scratch_plan_);
+  }
+  debug_ = flags;
   dump_dir_ = dump_dir;
   dump_runs_ = 0;
 }
@@ -454,8 +459,64 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
   }
 
   const int out_kind_boundary = graph_.output_fp32 ? kOutNchwF32 : kOutNchwF16;
+  // Residual-block fusion: conv i (64 -> 64, any activation, no residual
+  // input) whose output only conv i + 1 reads, as its input; conv i + 1
+  // (64 -> 64, no activation, up to two residual inputs) writes an internal
+  // tensor. Both run as one winograd_block launch and conv i's output is never
+  // materialized.
+  auto readers = [&](const std::string& t) {
+    int r = 0;
+    for (const Op& o : ops) {
+      r += (o.in0 == t) + (o.in1 == t);
+      for (const auto& sk : o.skips) r += sk == t;
+    }
+    return r;
+  };
+  auto conv_cm = [&](const Op& o, int64_t& c, int64_t& m) {
+    const Weight& w = graph_.weights.at(o.weight);
+    m = w.dims[0];
+    c = w.dims[1];
+  };
+  auto block_at = [&](int i) -> bool {
+    if ((debug_ & kDebugUnfused) || i + 1 >= nops) return false;
+    const Op& a = ops[i];
+    const Op& b = ops[i + 1];
+    if (a.kind != OpKind::Conv || b.kind != OpKind::Conv || i == fused_in_op) return false;
+    if (!a.skips.empty() || a.clip || a.dts_b >= 1 || b.clip || b.dts_b >= 1) return false;
+    if (b.act != kActNone || b.skips.size() > 2 || b.in0 != a.out) return false;
+    if (a.out == graph_.output_name || readers(a.out) != 1) return false;
+    if (direct_out && i + 1 == final_op) return false;
+    int64_t c1, m1, c2, m2;
+    conv_cm(a, c1, m1);
+    conv_cm(b, c2, m2);
+    if (c1 != 64 || m1 != 64 || c2 != 64 || m2 != 64) return false;
+    const Shape si = shapes.at(a.in0);
+    return block_eligible(64, 64, a.act, kActNone, si.n, si.h, si.w);
+  };
   for (int i = 0; i < nops; ++i) {
     const Op& op = ops[i];
+    if (block_at(i)) {
+      const Op& op2 = ops[i + 1];
+      const Shape si = shapes.at(op.in0);
+      // Producer index i: the output must not reuse a buffer conv i reads.
+      if (!alloc(op2.out, shapes.at(op2.out), i)) return fail();
+      Step st;
+      st.kind = StepKind::ConvBlock;
+      st.op = i;
+      st.op2 = i + 1;
+      st.in = tbuf.at(op.in0);
+      st.out = tbuf.at(op2.out);
+      st.N = (int32_t)si.n; st.H = (int32_t)si.h; st.W = (int32_t)si.w; st.C = 64; st.M = 64;
+      st.wbuf = op_wbuf_.at(i);
+      st.bbuf = op_bbuf_.at(i);
+      st.wbuf2 = op_wbuf_.at(i + 1);
+      st.bbuf2 = op_bbuf_.at(i + 1);
+      for (size_t k = 0; k < op2.skips.size(); ++k) st.skip[k] = tbuf.at(op2.skips[k]);
+      st.epi.act = op.act;
+      p.steps.push_back(st);
+      ++i;
+      continue;
+    }
     const Shape si = shapes.at(op.in0);
     const Shape so = shapes.at(op.out);
     const bool to_boundary = direct_out && i == final_op;
@@ -676,6 +737,22 @@ bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream
         }
         break;
       }
+      case StepKind::ConvBlock: {
+        BlockArgs a{};
+        a.in = static_cast<const uint16_t*>(ptr(st.in));
+        a.u1 = static_cast<const uint16_t*>(wbufs_[st.wbuf].ptr);
+        a.bias1 = static_cast<const float*>(wbufs_[st.bbuf].ptr);
+        a.u2 = static_cast<const uint16_t*>(wbufs_[st.wbuf2].ptr);
+        a.bias2 = static_cast<const float*>(wbufs_[st.bbuf2].ptr);
+        a.skip0 = static_cast<const uint16_t*>(ptr(st.skip[0]));
+        a.skip1 = static_cast<const uint16_t*>(ptr(st.skip[1]));
+        a.out = static_cast<uint16_t*>(ptr(st.out));
+        a.N = st.N; a.H = st.H; a.W = st.W;
+        a.act1 = st.epi.act;
+        a.act2 = kActNone;
+        e = launch_block(a, s);
+        break;
+      }
       case StepKind::Eltwise: {
         EltArgs a{};
         a.a = static_cast<const uint16_t*>(ptr(st.in));
@@ -785,6 +862,11 @@ std::string Engine::StepName(const Step& st) const {
         if (st.skip[k] != kNoBuffer) os << " +skip";
       if (st.epi.dts_b) os << " +dts" << st.epi.dts_b;
       if (st.epi.do_clip) os << " +clip";
+      break;
+    case StepKind::ConvBlock:
+      os << "winograd_block C64 M64" << acts[st.epi.act];
+      for (int k = 0; k < 2; ++k)
+        if (st.skip[k] != kNoBuffer) os << " +skip";
       break;
     case StepKind::Eltwise: os << "eltwise op" << st.elt_op << (st.binary ? " binary" : ""); break;
     case StepKind::DepthToSpace: os << "depth_to_space b" << st.dts_b; break;

@@ -35,9 +35,18 @@ enum DebugFlag : int {
   kDebugPoison = 1,    // before each run, fill every activation interior with fp16 NaN
   kDebugSyncEach = 2,  // synchronize the launch stream after every launch
   kDebugDump = 4,      // write each launch's inputs and output (first two runs)
+  kDebugUnfused = 8,   // run every conv as its own launch (no residual-block fusion)
 };
 
-enum class StepKind { InputConvert, ConvWinograd, ConvDirect, Eltwise, DepthToSpace, OutputConvert };
+enum class StepKind {
+  InputConvert,
+  ConvWinograd,
+  ConvDirect,
+  ConvBlock,  // two 64 -> 64 convs fused (winograd_block): op, op2
+  Eltwise,
+  DepthToSpace,
+  OutputConvert
+};
 
 // Buffer reference inside a plan: an index into Engine::bufs_, or the
 // boundary input/output supplied per run.
@@ -47,10 +56,12 @@ constexpr int kNoBuffer = -1;
 
 struct Step {
   StepKind kind = StepKind::ConvWinograd;
-  int op = -1;  // index into Graph::ops (-1 for IO steps)
+  int op = -1;   // index into Graph::ops (-1 for IO steps)
+  int op2 = -1;  // ConvBlock: the second conv
   int in = kNoBuffer, in2 = kNoBuffer, out = kNoBuffer;
   int skip[2] = {kNoBuffer, kNoBuffer};
   int wbuf = kNoBuffer, bbuf = kNoBuffer;  // packed weights / padded bias (weight cache)
+  int wbuf2 = kNoBuffer, bbuf2 = kNoBuffer;  // ConvBlock: the second conv's
   // Geometry of the step's input (NHWC) and channel counts.
   int32_t N = 0, H = 0, W = 0, C = 0, M = 0;
   Epilogue epi{};  // conv epilogue (pointers resolved per run)

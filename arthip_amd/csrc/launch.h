@@ -17,6 +17,11 @@ int winograd_max_m();   // output channels
 
 hipError_t launch_winograd(WinoArgs a, hipStream_t s);
 hipError_t launch_direct(DirectArgs a, hipStream_t s);
+// Fused residual block (winograd_block): C = M = 64, act2 none, act1 none /
+// ReLU / SiLU, 0-2 residual inputs. block_eligible says whether a block of this
+// geometry runs fused; launch_block refuses what it does not accept.
+bool block_eligible(int C, int M, int act1, int act2, int64_t N, int64_t H, int64_t W);
+hipError_t launch_block(BlockArgs a, hipStream_t s);
 hipError_t launch_eltwise(EltArgs a, bool binary, hipStream_t s);
 hipError_t launch_dts(DtsArgs a, hipStream_t s);
 hipError_t launch_input_convert(IoArgs a, hipStream_t s);

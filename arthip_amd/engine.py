@@ -205,13 +205,14 @@ class Engine:
         return [(labels[i], ms[i], cnt[i]) for i in range(min(n, cap))]
 
     # -- diagnostics --------------------------------------------------------------
-    DEBUG_POISON, DEBUG_SYNC_EACH, DEBUG_DUMP = 1, 2, 4
+    DEBUG_POISON, DEBUG_SYNC_EACH, DEBUG_DUMP, DEBUG_UNFUSED = 1, 2, 4, 8
 
     def set_debug(self, flags: int = 0, dump_dir=None) -> None:
         """The reference's VSHIP_POISON / VSHIP_SYNC_EACH / VSHIP_DUMP switches
         (hip_engine.cc:1310-1349): POISON fills every activation interior with
         fp16 NaN before each run, SYNC_EACH synchronizes after every launch, DUMP
-        writes each launch's inputs and output under dump_dir (first two runs)."""
+        writes each launch's inputs and output under dump_dir (first two runs),
+        UNFUSED runs every conv as its own launch (no residual-block fusion)."""
         d = str(dump_dir).encode() if dump_dir is not None else None
         if self._lib.arthip_engine_set_debug(self._h, int(flags), d) != 0:
             raise EngineError(_lib.last_error() or "set_debug failed")

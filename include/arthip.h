@@ -134,10 +134,15 @@ int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_
  *   output buffer are written to dump_dir/runR_opKK_inI.bin and
  *   runR_opKK_out.bin (raw bytes; internal activations in the padded NHWC
  *   fp16 layout of arthip_padded_dims, boundary tensors as given).
+ * - UNFUSED (no environment switch): every conv runs as its own launch; by
+ *   default a 64 -> 64 conv whose output only the next 64 -> 64 conv reads
+ *   runs fused with it (arthip_conv3x3_block_f16_nhwc), which agrees with
+ *   separate launches to fp16 rounding. Changing it drops the cached plans.
  * Returns 1 on an unknown flag or DUMP without a directory. */
 #define ARTHIP_DEBUG_POISON 1
 #define ARTHIP_DEBUG_SYNC_EACH 2
 #define ARTHIP_DEBUG_DUMP 4
+#define ARTHIP_DEBUG_UNFUSED 8
 int arthip_engine_set_debug(arthip_engine* eng, int flags, const char* dump_dir);
 int arthip_engine_get_debug(const arthip_engine* eng, int* flags);
 
@@ -329,6 +334,23 @@ int arthip_padded_dims(int H, int W, int* Hp, int* Wp);
 int arthip_conv3x3_f16_nhwc(const void* in, const void* packed, const float* bias, int act,
                             const void* skip0, const void* skip1, void* out, int N, int H, int W,
                             int C, int M, void* stream);
+
+/* A residual block of two fused 3x3 convs, C = M = 64:
+ *   out = skip1 + skip0 + conv3x3_2(act1(conv3x3_1(in) + bias1)) + bias2
+ * on padded NHWC fp16 device buffers of one geometry; the intermediate tensor
+ * never leaves the chip. The fused form of the reference's two winograd_conv
+ * launches with the residual Add fused into the second
+ * (src/common/hip_kernels.h:143-396; hip_graph.cc:510-540). The intermediate
+ * is computed with Winograd tiles at odd pixel offsets, so the result agrees
+ * with two arthip_conv3x3_f16_nhwc calls to fp16 rounding (same error against
+ * an exact reference), not bit for bit; it is bit-stable. packed1 / bias1 and packed2 /
+ * bias2 come from arthip_conv3x3_pack. act1: 0 none, 1 ReLU, 2 SiLU. skip1
+ * only with skip0; out must not alias in or a skip. Returns 1 for other
+ * channel counts or a padded image of 2 GiB or more. */
+int arthip_conv3x3_block_f16_nhwc(const void* in, const void* packed1, const float* bias1,
+                                  int act1, const void* packed2, const float* bias2,
+                                  const void* skip0, const void* skip1, void* out, int N, int H,
+                                  int W, int C, void* stream);
 
 /* Largest (C, M) the conv kernels accept. */
 int arthip_conv3x3_limits(int* max_c, int* max_m);

@@ -157,7 +157,7 @@ def test_debug_switches_without_a_gpu(tmp_path, monkeypatch):
     e.set_debug(Engine.DEBUG_POISON | Engine.DEBUG_DUMP, tmp_path)
     assert e.debug_flags() == 5
     with pytest.raises(EngineError):
-        e.set_debug(8)
+        e.set_debug(16)
     with pytest.raises(EngineError):
         e.set_debug(Engine.DEBUG_DUMP)  # no directory
     e.set_debug(0)

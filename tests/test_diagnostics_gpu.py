@@ -85,19 +85,23 @@ def _padded(h, w):
     return 2 * ((h + 1) // 2) + 2, 2 * ((w + 1) // 2) + 2
 
 
-def test_dump_writes_every_launch_of_the_first_two_runs(tmp_path):
-    """R8F64 at 20x28: 18 launches (head conv on the NCHW input, 16 body convs,
-    tail conv with DepthToSpace into the NCHW output). Each launch's output
-    buffer is the padded NHWC activation with a zero border and a finite
-    interior; consecutive launches see the same bytes; the head's input dump is
-    the boundary input and the tail's output dump the returned output. Only
-    the first two runs are dumped."""
+@pytest.mark.parametrize("fused", [False, True], ids=["unfused", "fused"])
+def test_dump_writes_every_launch_of_the_first_two_runs(tmp_path, fused):
+    """R8F64 at 20x28: 18 launches with every conv alone (head conv on the NCHW
+    input, 16 body convs, tail conv with DepthToSpace into the NCHW output), 10
+    with the residual blocks fused. Each launch's output buffer is the padded
+    NHWC activation with a zero border and a finite interior; consecutive
+    launches see the same bytes; the head's input dump is the boundary input and
+    the tail's output dump the returned output. Only the first two runs are
+    dumped."""
     spec = models.r8f64(seed=0)
     x = models.synthetic_input((1, 1, 20, 28), seed=1)
     hp, wp = _padded(20, 28)
+    n_launch = 10 if fused else 18
+    flags = Engine.DEBUG_DUMP | Engine.DEBUG_POISON | (0 if fused else Engine.DEBUG_UNFUSED)
     with Engine(0) as e:
         e.build(spec)
-        e.set_debug(Engine.DEBUG_DUMP | Engine.DEBUG_POISON, tmp_path)
+        e.set_debug(flags, tmp_path)
         outs = [e.run(x) for _ in range(3)]
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint16), outs[0].view(np.uint16))
@@ -105,12 +109,12 @@ def test_dump_writes_every_launch_of_the_first_two_runs(tmp_path):
     assert not any(f.startswith("run3_") for f in files), files
     for run in (1, 2):
         outs_run = sorted(f for f in files if f.startswith(f"run{run}_") and f.endswith("_out.bin"))
-        assert len(outs_run) == 18, outs_run
+        assert len(outs_run) == n_launch, outs_run
         head_in = (tmp_path / f"run{run}_op00_in0.bin").read_bytes()
         assert head_in == x.tobytes()
-        tail_out = (tmp_path / f"run{run}_op17_out.bin").read_bytes()
+        tail_out = (tmp_path / f"run{run}_op{n_launch - 1:02d}_out.bin").read_bytes()
         assert tail_out == outs[0].tobytes()
-        for k in range(17):
+        for k in range(n_launch - 1):
             a = np.frombuffer((tmp_path / f"run{run}_op{k:02d}_out.bin").read_bytes(),
                               np.float16).reshape(1, hp, wp, 64)
             border = a.copy()
