@@ -359,7 +359,16 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
     for (const auto& s : o.skips) r = r || s == graph_.output_name;
     output_read_inside = output_read_inside || r;
   }
-  const bool direct_out = final_op >= 0 && !output_read_inside &&
+  // A final conv with more than 16 outputs and no fused DepthToSpace or Clip
+  // writes the padded layout on the fast body kernels instead; the tiled output
+  // conversion then moves it to the boundary (the conv kernels' general
+  // boundary epilogue stores one element at a time).
+  bool final_wide = false;
+  if (final_op >= 0 && ops[final_op].kind == OpKind::Conv) {
+    const Op& fo = ops[final_op];
+    final_wide = graph_.weights.at(fo.weight).dims[0] > 16 && fo.dts_b < 1 && !fo.clip;
+  }
+  const bool direct_out = final_op >= 0 && !output_read_inside && !final_wide &&
                           (ops[final_op].kind == OpKind::Conv ||
                            ops[final_op].kind == OpKind::DepthToSpace);
 

@@ -265,11 +265,8 @@ __device__ __forceinline__ void item_coords(const WinoSched& sc, int sb, int nti
 // CVEC:  C % 4 == 0 (8-byte input loads).
 // FAST:  padded NHWC output with M % 4 == 0 and no clip (the inner layers);
 //        else the general epilogue (boundary layouts, fused DepthToSpace, odd M).
-// PF:    exactly one input task per thread: the next item's patch is
-//        prefetched into registers while the current item runs on MFMA.
-template <int KC, bool CVEC, bool FAST, bool PF>
+template <int KC, bool CVEC, bool FAST>
 __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
-  constexpr bool SKIP_PF = false;
   extern __shared__ __attribute__((aligned(16))) _Float16 vlds[];
   constexpr int CP = KC * 32;  // padded input channels
   constexpr int TS = CP + 8;   // LDS halfs per tile row (16-byte pad)
@@ -313,17 +310,12 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
   int n, th, tw0;
   item_coords(sc, sb, ntile, n, th, tw0);
   h4 d[16];
-  if (PF) load_task<KC, CVEC>(a, n, th, tw0, tid, d);
 
   for (;;) {
     // ---- input transform into LDS
-    if (PF) {
-      store_v<KC>(vlds, wps, tid, d);
-    } else {
-      for (int task = tid; task < ntask; task += blockDim.x) {
-        load_task<KC, CVEC>(a, n, th, tw0, task, d);
-        store_v<KC>(vlds, wps, task, d);
-      }
+    for (int task = tid; task < ntask; task += blockDim.x) {
+      load_task<KC, CVEC>(a, n, th, tw0, task, d);
+      store_v<KC>(vlds, wps, task, d);
     }
     lds_sync();
 
@@ -331,7 +323,6 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
     const bool more = nsb < sb_end;
     int nn = n, nth = th, ntw0 = tw0;
     if (more) item_coords(sc, nsb, ntile, nn, nth, ntw0);
-    if (PF && more) load_task<KC, CVEC>(a, nn, nth, ntw0, tid, d);
 
     const int tw = tw0 + tcol;
     const bool valid = (ch0 < a.M) && (tw < a.tiles_w);
@@ -339,8 +330,8 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
     const bool h1 = oh + 1 < a.H, w1 = ow + 1 < a.W;
     const int64_t ppix = ((int64_t)n * a.Hp + oh + 1) * a.Wp + ow + 1;
     const int64_t prow = (int64_t)a.Wp * a.M;
-    // Residual inputs for the fast epilogue. SKIP_PF requests them before the
-    // MFMA work (16 more live VGPRs); otherwise they load in the epilogue.
+    // Residual inputs for the fast epilogue, loaded after the MFMA work (before
+    // it they would hold 16 more VGPRs across it).
     h4 sk[2][4];
     auto load_skips = [&]() {
 #pragma unroll
@@ -359,7 +350,6 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
         }
       }
     };
-    if (FAST && SKIP_PF) load_skips();
 
     // ---- 16 position GEMMs on MFMA, folded row by row into the 2x2 tile
     f4 y[4];
@@ -405,7 +395,7 @@ __global__ void __launch_bounds__(512) winograd_conv(WinoArgs a, WinoSched sc) {
     }
 
     // ---- epilogue: lane holds 4 channels x the 4 pixels of one tile
-    if (FAST && !SKIP_PF) load_skips();
+    if (FAST) load_skips();
     if (valid) {
       if (FAST) {
         _Float16* o = reinterpret_cast<_Float16*>(a.epi.out) + ppix * a.M + ch0;
@@ -2622,6 +2612,68 @@ __global__ void __launch_bounds__(256) input_convert(IoArgs a) {
   }
 }
 
+// Multi-channel boundary conversions, tiled through LDS: a workgroup moves one
+// row segment of 64 pixels x C channels (blockIdx.x = segment, then row, then
+// image). The NCHW side is accessed per channel (64 consecutive pixels), the
+// padded NHWC side per pixel (C consecutive channels), both coalesced; a
+// one-element element-by-element conversion would scatter one of them.
+// LDS rows hold one pixel's C channels plus one pad element.
+constexpr int kIoSeg = 64;
+
+__global__ void __launch_bounds__(256) input_convert_tiled(IoArgs a) {
+  extern __shared__ _Float16 iolds[];
+  const int C = a.C, cs = a.C + 1;
+  const int nseg = (a.W + kIoSeg - 1) / kIoSeg;
+  const int seg = blockIdx.x % nseg;
+  const int64_t rest = blockIdx.x / nseg;
+  const int h = (int)(rest % a.H);
+  const int64_t n = rest / a.H;
+  const int w0 = seg * kIoSeg;
+  const int npx = min(kIoSeg, a.W - w0);
+  for (int i = threadIdx.x; i < C * kIoSeg; i += blockDim.x) {
+    const int c = i / kIoSeg, x = i - c * kIoSeg;
+    if (x >= npx) continue;
+    const int64_t src = ((n * C + c) * a.H + h) * a.W + w0 + x;
+    iolds[x * cs + c] = a.fp32 ? (_Float16)reinterpret_cast<const float*>(a.src)[src]
+                               : reinterpret_cast<const _Float16*>(a.src)[src];
+  }
+  __syncthreads();
+  _Float16* dst = reinterpret_cast<_Float16*>(a.dst) + ((n * a.Hp + h + 1) * a.Wp + w0 + 1) * C;
+  for (int i = threadIdx.x; i < npx * C; i += blockDim.x) {
+    const int x = i / C, c = i - x * C;
+    dst[i] = iolds[x * cs + c];
+  }
+}
+
+__global__ void __launch_bounds__(256) output_convert_tiled(IoArgs a) {
+  extern __shared__ _Float16 iolds[];
+  const int C = a.C, cs = a.C + 1;
+  const int nseg = (a.W + kIoSeg - 1) / kIoSeg;
+  const int seg = blockIdx.x % nseg;
+  const int64_t rest = blockIdx.x / nseg;
+  const int h = (int)(rest % a.H);
+  const int64_t n = rest / a.H;
+  const int w0 = seg * kIoSeg;
+  const int npx = min(kIoSeg, a.W - w0);
+  const _Float16* src =
+      reinterpret_cast<const _Float16*>(a.src) + ((n * a.Hp + h + 1) * a.Wp + w0 + 1) * C;
+  for (int i = threadIdx.x; i < npx * C; i += blockDim.x) {
+    const int x = i / C, c = i - x * C;
+    iolds[x * cs + c] = src[i];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < C * kIoSeg; i += blockDim.x) {
+    const int c = i / kIoSeg, x = i - c * kIoSeg;
+    if (x >= npx) continue;
+    const int64_t dst = ((n * C + c) * a.H + h) * a.W + w0 + x;
+    const _Float16 v = iolds[x * cs + c];
+    if (a.fp32)
+      reinterpret_cast<float*>(a.dst)[dst] = (float)v;
+    else
+      reinterpret_cast<_Float16*>(a.dst)[dst] = v;
+  }
+}
+
 // Padded NHWC fp16 -> boundary NCHW (fp16 or fp32).
 __global__ void __launch_bounds__(256) output_convert(IoArgs a) {
   const int64_t total = (int64_t)a.N * a.C * a.H * a.W;
@@ -2757,20 +2809,16 @@ FastDiv make_fastdiv(uint32_t d) {
 using WinoKernel = void (*)(WinoArgs, WinoSched);
 
 template <int KC>
-WinoKernel pick_kernel(bool cvec, bool fast, bool pf) {
-  if (cvec) {
-    if (fast) return pf ? winograd_conv<KC, true, true, true> : winograd_conv<KC, true, true, false>;
-    return pf ? winograd_conv<KC, true, false, true> : winograd_conv<KC, true, false, false>;
-  }
-  if (fast) return pf ? winograd_conv<KC, false, true, true> : winograd_conv<KC, false, true, false>;
-  return pf ? winograd_conv<KC, false, false, true> : winograd_conv<KC, false, false, false>;
+WinoKernel pick_kernel(bool cvec, bool fast) {
+  if (cvec) return fast ? winograd_conv<KC, true, true> : winograd_conv<KC, true, false>;
+  return fast ? winograd_conv<KC, false, true> : winograd_conv<KC, false, false>;
 }
 
-WinoKernel wino_kernel(int kc, bool cvec, bool fast, bool pf) {
+WinoKernel wino_kernel(int kc, bool cvec, bool fast) {
   switch (kc) {
-    case 1: return pick_kernel<1>(cvec, fast, pf);
-    case 2: return pick_kernel<2>(cvec, fast, pf);
-    case 3: return pick_kernel<3>(cvec, fast, pf);
+    case 1: return pick_kernel<1>(cvec, fast);
+    case 2: return pick_kernel<2>(cvec, fast);
+    case 3: return pick_kernel<3>(cvec, fast);
     default: return nullptr;
   }
 }
@@ -3001,12 +3049,7 @@ hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
   const bool cvec = (a.C % 4) == 0;
   const bool fast = a.epi.out_kind == kOutPadded && a.epi.dts_b < 2 && (a.M % 4) == 0 &&
                     !a.epi.do_clip;
-  // Register prefetch of the next item's patch costs 32 VGPRs; on top of the
-  // 128-VGPR U' slice (C = 64) that spills to scratch, and every reload then
-  // waits on all outstanding memory traffic. Measured on R8F64 1080p: 373 us per
-  // 64->64 ReLU layer with the prefetch vs 218 us without, so it stays off.
-  const bool pf = false;
-  WinoKernel fn = wino_kernel(g.kc, cvec, fast, pf);
+  WinoKernel fn = wino_kernel(g.kc, cvec, fast);
   if (fn == nullptr) return hipErrorInvalidValue;
   if (g.lds > 65536) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
@@ -3195,14 +3238,35 @@ hipError_t launch_dts(DtsArgs a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Tiled conversions for 2 <= C <= 128 (one workgroup per 64-pixel row
+// segment, at most 2^31 of them); otherwise one thread per element.
+static bool io_tiled(const IoArgs& a) {
+  const int64_t blocks = (int64_t)a.N * a.H * ((a.W + kIoSeg - 1) / kIoSeg);
+  return a.C >= 2 && a.C <= 128 && blocks < ((int64_t)1 << 31);
+}
+
 hipError_t launch_input_convert(IoArgs a, hipStream_t s) {
   const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  if (total == 0) return hipSuccess;
+  if (io_tiled(a)) {
+    const int64_t blocks = (int64_t)a.N * a.H * ((a.W + kIoSeg - 1) / kIoSeg);
+    const size_t lds = (size_t)kIoSeg * (a.C + 1) * 2;
+    hipLaunchKernelGGL(input_convert_tiled, dim3((unsigned)blocks), dim3(256), lds, s, a);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(input_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_output_convert(IoArgs a, hipStream_t s) {
   const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
+  if (total == 0) return hipSuccess;
+  if (io_tiled(a)) {
+    const int64_t blocks = (int64_t)a.N * a.H * ((a.W + kIoSeg - 1) / kIoSeg);
+    const size_t lds = (size_t)kIoSeg * (a.C + 1) * 2;
+    hipLaunchKernelGGL(output_convert_tiled, dim3((unsigned)blocks), dim3(256), lds, s, a);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(output_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
