@@ -2613,11 +2613,100 @@ __global__ void __launch_bounds__(256) input_convert(IoArgs a) {
 }
 
 // Multi-channel boundary conversions, tiled through LDS: a workgroup moves one
-// row segment of 64 pixels x C channels (blockIdx.x = segment, then row, then
-// image). The NCHW side is accessed per channel (64 consecutive pixels), the
-// padded NHWC side per pixel (C consecutive channels), both coalesced; a
-// one-element element-by-element conversion would scatter one of them.
-// LDS rows hold one pixel's C channels plus one pad element.
+// row segment of pixels x C channels (blockIdx.x = segment, then row, then
+// image). The NCHW side is accessed per channel (consecutive pixels), the
+// padded NHWC side per pixel (C consecutive channels), both coalesced; an
+// element-by-element conversion would scatter one of them.
+//
+// Vector form (C % 8 == 0, W % 8 == 0, so every 8-element group is 16-byte
+// aligned on both sides): 128-pixel segments, each lane moves 8 elements per
+// global access. LDS holds the segment channel-major, [c][x], rows of
+// kIoVecRow halfs (an odd number of dwords): the 8 channels of one pixel that a
+// lane gathers, and the 8 lanes of one pixel's channel groups, fall in
+// distinct banks.
+constexpr int kIoVecSeg = 128;
+constexpr int kIoVecRow = kIoVecSeg + 2;
+
+__global__ void __launch_bounds__(256) input_convert_vec(IoArgs a) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 iolds[];
+  const int C = a.C, cg = a.C >> 3;
+  const int nseg = (a.W + kIoVecSeg - 1) / kIoVecSeg;
+  const int seg = blockIdx.x % nseg;
+  const int64_t rest = blockIdx.x / nseg;
+  const int h = (int)(rest % a.H);
+  const int64_t n = rest / a.H;
+  const int w0 = seg * kIoVecSeg;
+  const int ng = min(kIoVecSeg, a.W - w0) >> 3;  // 8-pixel groups in the segment
+  // Load: task = (channel c, pixel group g), g fastest.
+  for (int i = threadIdx.x; i < C * (kIoVecSeg / 8); i += blockDim.x) {
+    const int c = i / (kIoVecSeg / 8), g = i - c * (kIoVecSeg / 8);
+    if (g >= ng) continue;
+    const int64_t src = ((n * C + c) * a.H + h) * a.W + w0 + 8 * g;
+    h8 v;
+    if (a.fp32) {
+      const f4* p = reinterpret_cast<const f4*>(reinterpret_cast<const float*>(a.src) + src);
+      const f4 lo = __builtin_nontemporal_load(p), hi = __builtin_nontemporal_load(p + 1);
+      v = h8{(_Float16)lo[0], (_Float16)lo[1], (_Float16)lo[2], (_Float16)lo[3],
+             (_Float16)hi[0], (_Float16)hi[1], (_Float16)hi[2], (_Float16)hi[3]};
+    } else {
+      v = __builtin_nontemporal_load(
+          reinterpret_cast<const h8*>(reinterpret_cast<const _Float16*>(a.src) + src));
+    }
+    const u4 w = __builtin_bit_cast(u4, v);
+    uint32_t* d = reinterpret_cast<uint32_t*>(iolds + c * kIoVecRow + 8 * g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[k] = w[k];
+  }
+  lds_sync();
+  // Store: task = (pixel x, channel group q), q fastest: a wave writes whole
+  // pixels, C * 2 consecutive bytes each.
+  _Float16* dst = reinterpret_cast<_Float16*>(a.dst) + ((n * a.Hp + h + 1) * a.Wp + w0 + 1) * C;
+  for (int i = threadIdx.x; i < 8 * ng * cg; i += blockDim.x) {
+    const int x = i / cg, q = i - x * cg;
+    h8 v;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = iolds[(8 * q + k) * kIoVecRow + x];
+    __builtin_nontemporal_store(v, reinterpret_cast<h8*>(dst + (int64_t)x * C + 8 * q));
+  }
+}
+
+__global__ void __launch_bounds__(256) output_convert_vec(IoArgs a) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 iolds[];
+  const int C = a.C, cg = a.C >> 3;
+  const int nseg = (a.W + kIoVecSeg - 1) / kIoVecSeg;
+  const int seg = blockIdx.x % nseg;
+  const int64_t rest = blockIdx.x / nseg;
+  const int h = (int)(rest % a.H);
+  const int64_t n = rest / a.H;
+  const int w0 = seg * kIoVecSeg;
+  const int ng = min(kIoVecSeg, a.W - w0) >> 3;
+  const _Float16* src =
+      reinterpret_cast<const _Float16*>(a.src) + ((n * a.Hp + h + 1) * a.Wp + w0 + 1) * C;
+  for (int i = threadIdx.x; i < 8 * ng * cg; i += blockDim.x) {
+    const int x = i / cg, q = i - x * cg;
+    const h8 v = __builtin_nontemporal_load(reinterpret_cast<const h8*>(src + (int64_t)x * C + 8 * q));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) iolds[(8 * q + k) * kIoVecRow + x] = v[k];
+  }
+  lds_sync();
+  for (int i = threadIdx.x; i < C * (kIoVecSeg / 8); i += blockDim.x) {
+    const int c = i / (kIoVecSeg / 8), g = i - c * (kIoVecSeg / 8);
+    if (g >= ng) continue;
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(iolds + c * kIoVecRow + 8 * g);
+    const h8 v = __builtin_bit_cast(h8, u4{sp[0], sp[1], sp[2], sp[3]});
+    const int64_t dst = ((n * C + c) * a.H + h) * a.W + w0 + 8 * g;
+    if (a.fp32) {
+      f4* p = reinterpret_cast<f4*>(reinterpret_cast<float*>(a.dst) + dst);
+      __builtin_nontemporal_store(f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}, p);
+      __builtin_nontemporal_store(f4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]}, p + 1);
+    } else {
+      __builtin_nontemporal_store(v, reinterpret_cast<h8*>(reinterpret_cast<_Float16*>(a.dst) + dst));
+    }
+  }
+}
+
+// Scalar form for any 2 <= C <= 128: 64-pixel segments, one element per lane
+// and access; LDS rows hold one pixel's C channels plus one pad element.
 constexpr int kIoSeg = 64;
 
 __global__ void __launch_bounds__(256) input_convert_tiled(IoArgs a) {
@@ -2637,7 +2726,7 @@ __global__ void __launch_bounds__(256) input_convert_tiled(IoArgs a) {
     iolds[x * cs + c] = a.fp32 ? (_Float16)reinterpret_cast<const float*>(a.src)[src]
                                : reinterpret_cast<const _Float16*>(a.src)[src];
   }
-  __syncthreads();
+  lds_sync();
   _Float16* dst = reinterpret_cast<_Float16*>(a.dst) + ((n * a.Hp + h + 1) * a.Wp + w0 + 1) * C;
   for (int i = threadIdx.x; i < npx * C; i += blockDim.x) {
     const int x = i / C, c = i - x * C;
@@ -2661,7 +2750,7 @@ __global__ void __launch_bounds__(256) output_convert_tiled(IoArgs a) {
     const int x = i / C, c = i - x * C;
     iolds[x * cs + c] = src[i];
   }
-  __syncthreads();
+  lds_sync();
   for (int i = threadIdx.x; i < C * kIoSeg; i += blockDim.x) {
     const int c = i / kIoSeg, x = i - c * kIoSeg;
     if (x >= npx) continue;
@@ -3238,20 +3327,33 @@ hipError_t launch_dts(DtsArgs a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Tiled conversions for 2 <= C <= 128 (one workgroup per 64-pixel row
-// segment, at most 2^31 of them); otherwise one thread per element.
+// Tiled conversions for 2 <= C <= 128 (one workgroup per row segment, at most
+// 2^31 of them); the vector form when C and W are multiples of 8 and both
+// buffers 16-byte aligned; otherwise one thread per element.
+static int64_t io_blocks(const IoArgs& a, int seg) {
+  return (int64_t)a.N * a.H * ((a.W + seg - 1) / seg);
+}
 static bool io_tiled(const IoArgs& a) {
-  const int64_t blocks = (int64_t)a.N * a.H * ((a.W + kIoSeg - 1) / kIoSeg);
-  return a.C >= 2 && a.C <= 128 && blocks < ((int64_t)1 << 31);
+  return a.C >= 2 && a.C <= 128 && io_blocks(a, kIoSeg) < ((int64_t)1 << 31);
+}
+static bool io_vec(const IoArgs& a) {
+  return io_tiled(a) && a.C % 8 == 0 && a.W % 8 == 0 &&
+         reinterpret_cast<uintptr_t>(a.src) % 16 == 0 && reinterpret_cast<uintptr_t>(a.dst) % 16 == 0;
 }
 
 hipError_t launch_input_convert(IoArgs a, hipStream_t s) {
   const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
   if (total == 0) return hipSuccess;
+  if (io_vec(a)) {
+    const size_t lds = (size_t)a.C * kIoVecRow * 2;
+    hipLaunchKernelGGL(input_convert_vec, dim3((unsigned)io_blocks(a, kIoVecSeg)), dim3(256), lds,
+                       s, a);
+    return hipGetLastError();
+  }
   if (io_tiled(a)) {
-    const int64_t blocks = (int64_t)a.N * a.H * ((a.W + kIoSeg - 1) / kIoSeg);
     const size_t lds = (size_t)kIoSeg * (a.C + 1) * 2;
-    hipLaunchKernelGGL(input_convert_tiled, dim3((unsigned)blocks), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(input_convert_tiled, dim3((unsigned)io_blocks(a, kIoSeg)), dim3(256), lds,
+                       s, a);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(input_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);
@@ -3261,10 +3363,16 @@ hipError_t launch_input_convert(IoArgs a, hipStream_t s) {
 hipError_t launch_output_convert(IoArgs a, hipStream_t s) {
   const int64_t total = (int64_t)a.N * a.H * a.W * a.C;
   if (total == 0) return hipSuccess;
+  if (io_vec(a)) {
+    const size_t lds = (size_t)a.C * kIoVecRow * 2;
+    hipLaunchKernelGGL(output_convert_vec, dim3((unsigned)io_blocks(a, kIoVecSeg)), dim3(256), lds,
+                       s, a);
+    return hipGetLastError();
+  }
   if (io_tiled(a)) {
-    const int64_t blocks = (int64_t)a.N * a.H * ((a.W + kIoSeg - 1) / kIoSeg);
     const size_t lds = (size_t)kIoSeg * (a.C + 1) * 2;
-    hipLaunchKernelGGL(output_convert_tiled, dim3((unsigned)blocks), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(output_convert_tiled, dim3((unsigned)io_blocks(a, kIoSeg)), dim3(256), lds,
+                       s, a);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(output_convert, dim3(grid_for(total, 256)), dim3(256), 0, s, a);

@@ -82,13 +82,17 @@ def parse():
                    help="instead of the bench, summarize rocprofv3 csv output under DIR "
                         "(DIR/kt: --kernel-trace --stats; DIR/fetch, DIR/write: --pmc "
                         "FETCH_SIZE / WRITE_SIZE; DIR/cal_fetch, DIR/cal_write: the same "
-                        "counters on --calibrate-copy) into per-launch figures of one frame; "
-                        "prints a markdown table and writes JSON to --profile-json")
+                        "counters on --calibrate-copy; optional DIR/p1, DIR/p2: the SQ "
+                        "counter passes listed in the output) into per-launch figures of one "
+                        "frame; prints markdown tables and writes JSON to --profile-json")
     p.add_argument("--profile-json", default="", metavar="FILE")
     p.add_argument("--profile-key", default="", metavar="KEY",
                    help="workload key of the summary, e.g. r8f64_1080x1920")
     p.add_argument("--frames", type=int, default=0,
                    help="with --summarize-profile: frames in the trace run (warmup + steps)")
+    p.add_argument("--skip-frames", type=int, default=0,
+                   help="with --summarize-profile: leading (warmup) frames of the trace run "
+                        "left out of the launch times")
     return p.parse_args()
 
 
@@ -309,10 +313,11 @@ def summarize_profile(args) -> int:
               file=sys.stderr)
         return 1
     per = len(trace) // frames
+    timed = trace[per * args.skip_frames:]
     launches = []
     for i in range(per):
         ts = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
-              for r in trace[i::per]]
+              for r in timed[i::per]]
         launches.append({"kernel": short(trace[i]["Kernel_Name"]),
                          "trace_mean_us": round(statistics.mean(ts), 2),
                          "trace_median_us": round(statistics.median(ts), 2)})
@@ -341,6 +346,13 @@ def summarize_profile(args) -> int:
             L["read_bytes"] = round(fetch[i] * 1024 * fscale)
             L["write_bytes"] = round(write[i] * 1024 * wscale)
             L["hbm_bytes"] = L["read_bytes"] + L["write_bytes"]
+    # SQ counter passes (MFMA, VALU, LDS, waits), averaged per kernel name.
+    sq = {}
+    for sub in ("p1", "p2"):
+        for r in rows(sub, "*counter_collection.csv"):
+            if engine(r["Kernel_Name"]):
+                sq.setdefault(short(r["Kernel_Name"]), {}).setdefault(
+                    r["Counter_Name"], []).append(float(r["Counter_Value"]))
     summary = {"launches": launches, "fetch_scale": fscale, "write_scale": wscale,
                "frames": frames}
     if args.profile_json:
@@ -354,7 +366,30 @@ def summarize_profile(args) -> int:
         print(f"| {i} | `{L['kernel']}` | {L['trace_mean_us']} | "
               f"{L.get('read_bytes', 0) / 1e6:.1f} | {L.get('write_bytes', 0) / 1e6:.1f} |")
     print(f"\nframe: {sum(L['trace_mean_us'] for L in launches):.1f} us of kernels "
-          f"({per} launches); FETCH scale {fscale}, WRITE scale {wscale}")
+          f"({per} launches, mean over {frames - args.skip_frames} frames); "
+          f"FETCH scale {fscale:.4f}, WRITE scale {wscale:.4f} (plain copy calibration)")
+    if sq:
+        def av(k, c):
+            v = sq[k].get(c)
+            return statistics.mean(v) if v else float("nan")
+        print("\n| kernel | trace us | MFMA util % | F16 MFMA GFLOP | LDS active % | "
+              "LDS bank conflicts | waiting % | VALU instr (M) | MFMA instr (M) | LDS instr (M) |")
+        print("|---|---|---|---|---|---|---|---|---|---|")
+        for k in dict.fromkeys(L["kernel"] for L in launches):
+            if k not in sq:
+                continue
+            gui = av(k, "GRBM_GUI_ACTIVE") / 8  # summed over the 8 XCDs
+            simds, cus = 1024, 256
+            mfma = av(k, "SQ_VALU_MFMA_BUSY_CYCLES") / (gui * simds) * 100
+            lds_act = av(k, "SQ_LDS_IDX_ACTIVE") / (gui * cus) * 100
+            conf = av(k, "SQ_LDS_BANK_CONFLICT")
+            conf_ratio = conf / max(av(k, "SQ_LDS_IDX_ACTIVE") - conf, 1.0)
+            wait = av(k, "SQ_WAIT_ANY") / av(k, "SQ_WAVE_CYCLES") * 100
+            tus = statistics.mean(L["trace_mean_us"] for L in launches if L["kernel"] == k)
+            print(f"| `{k}` | {tus:.1f} | {mfma:.1f} | "
+                  f"{av(k, 'SQ_INSTS_VALU_MFMA_MOPS_F16') * 512 / 1e9:.1f} | {lds_act:.1f} | "
+                  f"{conf_ratio:.3f} | {wait:.0f} | {av(k, 'SQ_INSTS_VALU') / 1e6:.2f} | "
+                  f"{av(k, 'SQ_INSTS_MFMA') / 1e6:.2f} | {av(k, 'SQ_INSTS_LDS') / 1e6:.2f} |")
     return 0
 
 

@@ -348,6 +348,36 @@ def test_boundary_tail_convs(filters, out_ch, scale, clip, io32):
         assert s["max_abs"] <= 2e-2, s
 
 
+@pytest.mark.parametrize("io32", [False, True])
+@pytest.mark.parametrize("cin,cout", [(8, 24), (12, 20), (24, 64), (64, 64), (64, 128)])
+def test_multichannel_boundary_conversions(cin, cout, io32):
+    """Multi-channel NCHW boundaries: the input goes through the tiled input
+    conversion (vector form when C and W are multiples of 8, scalar form
+    otherwise) and a final conv with more than 16 outputs through the tiled
+    output conversion. Widths cover a whole number of 128-pixel segments, a
+    partial last segment and widths that are not a multiple of 8."""
+    b = models._Builder(11, "uniform", io32)
+    xin = "xh" if io32 else "x"
+    y = b.conv(xin, cin, cout)
+    m = b.finish(xin, y, cin, cout)
+    for h, w in [(5, 256), (6, 200), (3, 70), (4, 13)]:
+        x = models.synthetic_input((1, cin, h, w), seed=h * w, kind="normal")
+        if io32:
+            x = x.astype(np.float32)
+        with Engine(0) as e:
+            got, names = _steps(e.build(m), x)
+        got = got.astype(np.float32)
+        assert any(n.startswith("input_convert") for n in names), names
+        assert any(n.startswith("output_convert") for n in names), names
+        want = run_model(m, x)
+        floor = run_model(m, x, round_fp16=False)
+        s, f = _compare(got, want), _compare(floor, want)
+        assert got.shape == want.shape == (1, cout, h, w), (got.shape, want.shape)
+        assert np.isfinite(got).all()
+        assert s["rel_rms"] <= max(FLOOR_RATIO * f["rel_rms"], 2e-3), ((h, w), s, f)
+        assert s["max_abs"] <= 2e-2 * max(1.0, float(np.abs(want).max())), ((h, w), s)
+
+
 def _steps(engine, x):
     engine.set_profiling(True)
     engine.profile_read()
