@@ -96,6 +96,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     sig("arthip_engine_build_subgraph", c_int, eng, c_void, c_size, i32p, c_int, c_char, c_int)
     sig("arthip_ep_run_boundary", c_int, c_void, c_size, i32p, c_int, c_char, c_int, i32p, c_char,
         c_int, i32p, c_char, c_int, i32p, c_char, c_int)
+    sig("arthip_ep_node_keys", c_int, c_void, c_size, i32p, c_int, c_char, c_int, c_char, c_int)
 
     fmtp = ctypes.POINTER(VsFormat)
     ptrs = ctypes.POINTER(c_void)
@@ -134,7 +135,8 @@ EXPORTED_SYMBOLS = (
     "arthip_engine_set_profiling", "arthip_engine_profile_read", "arthip_engine_set_debug",
     "arthip_engine_get_debug",
     "engine_device_count", "engine_probe", "engine_run", "engine_alloc_failure_then_run",
-    "arthip_ep_get_capability", "arthip_ep_run_boundary", "arthip_engine_build_subgraph",
+    "arthip_ep_get_capability", "arthip_ep_run_boundary", "arthip_ep_node_keys",
+    "arthip_engine_build_subgraph",
     "arthip_vs_model_create", "arthip_vs_model_get_frame", "arthip_vs_model_destroy",
     "arthip_vs_version", "arthip_vs_device_properties",
     "arthip_conv3x3_packed_halfs", "arthip_conv3x3_bias_len", "arthip_conv3x3_pack",

@@ -442,6 +442,24 @@ int arthip_ep_run_boundary(const void* model, size_t size, const int* nodes, int
   });
 }
 
+int arthip_ep_node_keys(const void* model, size_t size, const int* nodes, int n_nodes,
+                        char* keys, int keys_len, char* err, int errlen) {
+  return guard(ARTHIP_ERR_BUILD, err, errlen, "", [&]() -> int {
+    if (model == nullptr || (n_nodes > 0 && nodes == nullptr))
+      return report("null model or node list", ARTHIP_ERR_BUILD, err, errlen);
+    arthip::onnx::Model m;
+    std::string e;
+    if (!arthip::onnx::ParseModel(model, size, m, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+    std::vector<std::string> names;
+    const std::vector<int> run(nodes, nodes + (n_nodes > 0 ? n_nodes : 0));
+    if (!arthip::EpNodeKeys(m, run, names, e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
+    if (!pack_names(names, keys, keys_len))
+      return report("key buffer is too small", ARTHIP_ERR_BUILD, err, errlen);
+    copy_out("", err, errlen);
+    return ARTHIP_OK;
+  });
+}
+
 int arthip_engine_build_subgraph(arthip_engine* eng, const void* model, size_t size,
                                  const int* nodes, int n_nodes, char* err, int errlen) {
   return guard(ARTHIP_ERR_BUILD, err, errlen, "", [&]() -> int {

@@ -246,6 +246,31 @@ bool EpRunBoundary(const onnx::Model& m, const std::vector<int>& run,
   return true;
 }
 
+bool EpNodeKeys(const onnx::Model& m, const std::vector<int>& nodes,
+                std::vector<std::string>& keys, std::string& error) {
+  keys.clear();
+  for (int i : nodes) {
+    if (i < 0 || i >= static_cast<int>(m.graph.nodes.size())) {
+      error = "node index " + std::to_string(i) + " is outside the graph";
+      return false;
+    }
+    const onnx::Node& n = m.graph.nodes[i];
+    const std::string* key = nullptr;
+    for (const auto& o : n.outputs)
+      if (!o.empty()) {
+        key = &o;
+        break;
+      }
+    if (key == nullptr) {
+      error = "node " + std::to_string(i) + " ('" + n.name + "', " + n.op_type +
+              ") has no output to name it by";
+      return false;
+    }
+    keys.push_back(*key);
+  }
+  return true;
+}
+
 bool EpRunModel(const onnx::Model& m, const std::vector<int>& run, onnx::Model& out,
                 std::string& error) {
   const auto& nodes = m.graph.nodes;

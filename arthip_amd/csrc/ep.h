@@ -47,6 +47,15 @@ bool EpRunBoundary(const onnx::Model& model, const std::vector<int>& nodes,
                    std::vector<std::string>& activations, std::vector<std::string>& constants,
                    std::vector<std::string>& outputs, std::string& error);
 
+// The key of each listed node: its first non-empty output name. ONNX lets one
+// node only produce a tensor name, so a key names one node of the graph in any
+// serialization of it and in the caller's own node list, whatever their order
+// and whatever nodes were added or removed elsewhere; node names may be empty
+// or repeated and positions change with the order. Fails for an index outside
+// the graph or a node without outputs.
+bool EpNodeKeys(const onnx::Model& model, const std::vector<int>& nodes,
+                std::vector<std::string>& keys, std::string& error);
+
 // The model of one run: its nodes, the initializers they read, and the run's
 // input and output as graph input and output with their inferred types.
 bool EpRunModel(const onnx::Model& model, const std::vector<int>& nodes, onnx::Model& out,

@@ -85,6 +85,21 @@ def run_boundary(model, nodes) -> tuple[list[str], list[str], list[str]]:
     return tuple([x.decode() for x in names(b, n)] for b, n in zip(bufs, counts))
 
 
+def node_keys(model, nodes) -> list[str]:
+    """Each listed node's key (its first non-empty output name), which names
+    the node in any node order of the same graph."""
+    lib = _lib.lib()
+    data = model_bytes(model)
+    buf = ctypes.create_string_buffer(data, len(data))
+    idx = (ctypes.c_int * max(len(nodes), 1))(*nodes)
+    out = ctypes.create_string_buffer(1 << 16)
+    e = _err()
+    rc = lib.arthip_ep_node_keys(buf, len(data), idx, len(nodes), out, len(out), e, _ERR_LEN)
+    if rc != 0:
+        raise EngineError(_msg(e, f"node_keys failed (rc={rc})"))
+    return [x.decode() for x in out.raw.split(b"\0")[:len(nodes)]] if nodes else []
+
+
 def _err() -> ctypes.Array:
     return ctypes.create_string_buffer(_ERR_LEN)
 

@@ -175,9 +175,22 @@ int arthip_ep_run_boundary(const void* model, size_t size, const int* nodes, int
                            char* constants, int constants_len, int* n_constants, char* outputs,
                            int outputs_len, int* n_outputs, char* err, int errlen);
 
+/* The key of each listed node, for mapping a run onto the caller's own graph
+ * (IndexedSubGraph::Nodes() takes ORT NodeIndex values,
+ * hip_execution_provider.cc:303-306): the node's first non-empty output name,
+ * NUL-separated in node order. ONNX gives every tensor name one producer, so
+ * a key names the same node in the caller's graph whatever its node order;
+ * node indices are positions in the serialized model only. Returns 1 for an
+ * index outside the graph, a node without outputs or a buffer too small. */
+int arthip_ep_node_keys(const void* model, size_t size, const int* nodes, int n_nodes,
+                        char* keys, int keys_len, char* err, int errlen);
+
 /* Compile for one claimed run (hip_execution_provider.cc:337-357): builds the
  * engine from the run's nodes of the serialized model, with the run's single
- * activation as input 0 and its single output as output 0. */
+ * activation as input 0 and its single output as output 0. The reference
+ * compiles the fused node's filtered graph; serialized on its own (its nodes,
+ * the run's inputs including the initializers, their initializers, the run's
+ * output), that graph is such a model with nodes 0 .. n-1. */
 int arthip_engine_build_subgraph(arthip_engine* eng, const void* model, size_t size,
                                  const int* nodes, int n_nodes, char* err, int errlen);
 

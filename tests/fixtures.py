@@ -59,6 +59,31 @@ def _model(nodes, in_name, in_shape, in_type, out_name, out_shape, out_type, ini
     return op.Model(graph=g, opset_imports=[("", OPSET)])
 
 
+def fused_node_graph(model, run):
+    """The fused node's own graph as ONNX Runtime hands it to Compile
+    (FusedNodeAndGraph::filtered_graph) and as the EP shim serializes it: the
+    run's nodes; as inputs the MetaDef inputs (the activation, then the
+    initializers); the initializers; the MetaDef output."""
+    from arthip_amd.engine import run_boundary
+    acts, consts, outs = run_boundary(model, run)
+    g = model.graph
+    inits = {t.name: t for t in g.initializers}
+    declared = {v.name: v for v in list(g.inputs) + list(g.outputs)}
+
+    def info(name):
+        if name in inits:
+            t = inits[name]
+            return op.value_info(name, t.data_type, list(t.dims))
+        if name in declared:
+            return declared[name]
+        return op.value_info(name, op.FLOAT16, None)
+
+    sub = op.Graph(nodes=[g.nodes[i] for i in run], name="fused",
+                   initializers=[inits[c] for c in consts],
+                   inputs=[info(n) for n in acts + consts], outputs=[info(n) for n in outs])
+    return op.Model(graph=sub, opset_imports=model.opset_imports)
+
+
 class FixtureSet:
     def __init__(self, out: Path):
         self.out = Path(out)

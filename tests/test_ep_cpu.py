@@ -19,7 +19,7 @@ import pytest
 
 from arthip_amd import onnx_proto as op
 from arthip_amd.engine import EngineError, get_capability
-from tests.fixtures import _conv, _half, _model, kern, linspace
+from tests.fixtures import _conv, _half, _model, fused_node_graph, kern, linspace
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 F16, F32 = op.FLOAT16, op.FLOAT
@@ -225,3 +225,113 @@ def test_run_boundary(fixtures):
         run_boundary(m, [1, 0])
     with pytest.raises(EngineError, match="empty"):
         run_boundary(m, [])
+
+
+# ---------------------------------------------------------------------------
+# Runs named by node keys, and the fused node's own graph
+# ---------------------------------------------------------------------------
+
+def _chain_after_prefix(order, cast_pair=False):
+    """An unsupported prefix (Tanh on the input, and a Shape node beside it whose
+    output is a second graph output), then the chain Conv -> Relu -> Conv that
+    the EP claims. `order` permutes the node list among valid topological
+    orders; `cast_pair` puts an fp16 -> fp32 -> fp16 Cast pair between the
+    prefix and the chain (unclaimed: neither Cast touches the graph boundary)."""
+    w1, w2 = kern(41, 8, 4), kern(42, 4, 8)
+    tanh = op.node("Tanh", ["x"], ["xt"])
+    shape = op.node("Shape", ["x"], ["shp"])
+    head_in = "xt"
+    casts = []
+    if cast_pair:
+        casts = [op.node("Cast", ["xt"], ["x32"], to=F32), op.node("Cast", ["x32"], ["x16"], to=F16)]
+        head_in = "x16"
+    chain = [_conv(head_in, "w1", None, "a"), op.node("Relu", ["a"], ["r"]),
+             _conv("r", "w2", None, "y")]
+    named = {"tanh": tanh, "shape": shape, "c1": chain[0], "relu": chain[1], "c2": chain[2]}
+    nodes = []
+    for key in order:
+        nodes.append(named[key])
+        if key == "tanh":
+            nodes.extend(casts)
+    g = op.Graph(nodes=nodes, name="prefix_chain",
+                 initializers=[_half("w1", w1), _half("w2", w2)],
+                 inputs=[op.value_info("x", F16, [1, 4, "h", "w"])],
+                 outputs=[op.value_info("y", F16, [1, 4, "h", "w"]),
+                          op.value_info("shp", op.INT64, [4])])
+    return op.Model(graph=g, opset_imports=[("", 17)])
+
+
+ORDERS = [["tanh", "shape", "c1", "relu", "c2"], ["shape", "tanh", "c1", "relu", "c2"],
+          ["tanh", "c1", "relu", "c2", "shape"]]
+
+
+def _runs_by_key(model):
+    from arthip_amd.engine import node_keys
+    return [node_keys(model, run) for run in claims(model)]
+
+
+def _resolve(keys, model):
+    """What an EP shim does with the keys: find each node in its own node list
+    (ONNX Runtime's graph) by output name."""
+    by_output = {}
+    for i, n in enumerate(model.graph.nodes):
+        for o in n.outputs:
+            if o:
+                by_output[o] = i
+    return [by_output[k] for k in keys]
+
+
+def test_runs_by_key_survive_node_order_and_removed_casts():
+    """The same claimed run, named by keys, in every node order and with a Cast
+    pair removed before it; its node positions change with all of these. Keys
+    resolved in another serialization's node list select the same Conv, Relu,
+    Conv; the positions of one serialization applied to another would not."""
+    variants = [_chain_after_prefix(o) for o in ORDERS]
+    variants += [_chain_after_prefix(o, cast_pair=True) for o in ORDERS[:2]]
+    positions = [claims(m) for m in variants]
+    assert positions == [[[2, 3, 4]], [[2, 3, 4]], [[1, 2, 3]], [[4, 5, 6]], [[4, 5, 6]]]
+    keyed = [_runs_by_key(m) for m in variants]
+    assert all(k == [["a", "r", "y"]] for k in keyed), keyed
+    for src in variants:
+        (keys,) = _runs_by_key(src)
+        for dst in variants:
+            picked = [dst.graph.nodes[i] for i in _resolve(keys, dst)]
+            assert [n.op_type for n in picked] == ["Conv", "Relu", "Conv"]
+            assert [n.outputs[0] for n in picked] == ["a", "r", "y"]
+    # Positions do not carry over: the third order's run, applied to the first
+    # order's node list, would pick the Shape node and drop the last Conv.
+    wrong = [variants[0].graph.nodes[i] for i in positions[2][0]]
+    assert [n.op_type for n in wrong] == ["Shape", "Conv", "Relu"]
+
+
+def test_node_keys_errors():
+    from arthip_amd.engine import node_keys
+    m = _chain_after_prefix(ORDERS[0])
+    assert node_keys(m, [0, 1]) == ["xt", "shp"]
+    assert node_keys(m, []) == []
+    with pytest.raises(EngineError, match="outside"):
+        node_keys(m, [5])
+    g = op.Graph(nodes=[op.node("Relu", ["x"], [""]), op.node("Relu", ["x"], ["y"])],
+                 inputs=[op.value_info("x", F16, [1, 4, "h", "w"])],
+                 outputs=[op.value_info("y", F16, [1, 4, "h", "w"])])
+    with pytest.raises(EngineError, match="no output"):
+        node_keys(op.Model(graph=g), [0])
+
+
+@pytest.mark.parametrize("which", ["shipped", "prefix_chain", "fp32io"])
+def test_fused_node_graph_is_claimed_whole(which, fixtures):
+    """Compile works from the fused node's own graph: serialized on its own, with
+    the initializers also listed as graph inputs, it is one claimed run of all
+    its nodes with the same MetaDef as the run in the whole model."""
+    from arthip_amd.engine import run_boundary
+    if which == "shipped":
+        m = op.load(GOLDEN / "ArtCNN_R8F64_fp16.onnx")
+    elif which == "prefix_chain":
+        m = _chain_after_prefix(ORDERS[1], cast_pair=True)
+    else:
+        m = op.load(fixtures.get("ep_conv_fp32io").model)
+    (run,) = claims(m)
+    sub = fused_node_graph(m, run)
+    n = len(sub.graph.nodes)
+    assert claims(sub) == [list(range(n))]
+    assert run_boundary(sub, list(range(n))) == run_boundary(m, run)

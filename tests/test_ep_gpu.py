@@ -18,7 +18,7 @@ import pytest
 
 from arthip_amd import onnx_proto as op
 from arthip_amd.engine import Engine, get_capability
-from tests.fixtures import _conv, _half, _model, kern
+from tests.fixtures import _conv, _half, _model, fused_node_graph, kern
 
 pytestmark = pytest.mark.gpu
 
@@ -73,3 +73,23 @@ def test_split_model_runs_like_the_fallback():
     want = run_model(m, x)
     assert y.shape == want.shape
     assert np.abs(y.astype(np.float64) - want).max() <= 2e-2
+
+
+@pytest.mark.parametrize("which", ["shipped", "fp32io"])
+def test_compile_from_the_fused_node_graph(which, fixtures):
+    """Compile as the EP shim does it: the fused node's own graph, serialized on
+    its own, built over all of its nodes, gives the same bits as the run built
+    from the whole model."""
+    if which == "shipped":
+        m = op.load(GOLDEN / "ArtCNN_R8F64_fp16.onnx")
+        x = np.load(GOLDEN / "shipped_luma_48x64.npz")["x"]
+    else:
+        m = op.load(fixtures.get("ep_conv_fp32io").model)
+        x = np.random.default_rng(4).uniform(-1, 1, (1, 1, 18, 30)).astype(np.float32)
+    (run,) = get_capability(m, device_id=0)
+    sub = fused_node_graph(m, run)
+    with Engine(0) as a, Engine(0) as b:
+        got = a.build_subgraph(sub, list(range(len(sub.graph.nodes)))).run(x)
+        want = b.build_subgraph(m, run).run(x)
+    assert got.dtype == want.dtype and got.shape == want.shape
+    np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
