@@ -557,6 +557,16 @@ struct IntC {
   static constexpr int value = N;
 };
 
+// f(IntC<0>{}), ..., f(IntC<N-1>{}): a loop whose index is a compile-time
+// constant in every iteration.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(IntC<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 // Two waves per SIMD: at most 256 registers per lane (U' takes 64 * KC).
 // Output staging: after act and the fp16 rounding, each item's 2 x 32 x C
 // output tile goes to LDS as [row][pixel][C] (16-byte channel groups of pixel x
@@ -2025,14 +2035,25 @@ conv3x3_tail(NarrowArgs a) {
   struct Row {
     h8 v[KC];
   };
-  auto load_row = [&](Row& R, int j) {
-    int pr = h0 + j;
+  // Window row j of the current run: padded row h0 + j walking down, or
+  // h0 + len + 1 - j walking up. Rows past the run's len + 2 are not fetched
+  // (out-of-range offset: the load returns zeros and reads no memory).
+  int len = 0;
+  auto load_row = [&](Row& R, int j, auto rev_tag) {
+    constexpr bool REV = decltype(rev_tag)::value;
+    int pr = REV ? h0 + len + 1 - j : h0 + j;
     if (pr > a.Hp - 1) pr = a.Hp - 1;
-    const uint32_t o = (uint32_t)pr * prow + aoff;
+    const uint32_t o = j < len + 2 ? (uint32_t)pr * prow + aoff : kOob;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc)
       R.v[kc] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(irs, o + 64 * kc, 0, 0));
   };
+  // A thread's four elements are consecutive output pixels of one output row
+  // when SEG * b is a multiple of 4 (b even); with Wo % 4 == 0 and an aligned
+  // output they go out as one 4-element store, except where the segment
+  // crosses the image's right edge.
+  const bool pack4 = (b & 1) == 0 && (Wo & 3) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.out) & (4 * ELEM - 1)) == 0;
   int pn = 0, ps = 0, ph = 0;
   auto store_item = [&](int tb, bool live) {
     char* ob = reinterpret_cast<char*>(a.out) + (int64_t)pn * a.img_bytes;
@@ -2040,17 +2061,37 @@ conv3x3_tail(NarrowArgs a) {
         __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, (int)a.img_bytes, 0x00020000);
     const uint32_t item_off = (uint32_t)(((int64_t)ph * b * Wo + (int64_t)SEG * ps * b) * ELEM);
     const float* tp = tile + tb * TILE;
+    float v[4];
+    bool ok[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = (tp[s_tile[i]] + tp[s_tile[i] + dxs]) + tp[s_tile[i] + 2 * dxs];
-      v = apply_act(v + s_bias[i], a.act);
-      if (a.do_clip) v = apply_clip(v, a.clip_lo, a.clip_hi);
-      const bool ok = live && s_live[i] && (SEG * ps + s_x[i] < a.W);
-      const uint32_t off = ok ? item_off + s_off[i] : kOob;
+      float t = (tp[s_tile[i]] + tp[s_tile[i] + dxs]) + tp[s_tile[i] + 2 * dxs];
+      t = apply_act(t + s_bias[i], a.act);
+      if (a.do_clip) t = apply_clip(t, a.clip_lo, a.clip_hi);
+      v[i] = t;
+      ok[i] = live && s_live[i] && (SEG * ps + s_x[i] < a.W);
+    }
+    // ok[] only falls along i (element index and pixel both rise), so ok[3]
+    // means all four.
+    if (pack4 && ok[3]) {
       if (F32) {
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, off, 0, 0);
+        const u4 q = {__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                      __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, rs, item_off + s_off[0], 0, 0);
       } else {
-        const _Float16 hv = (_Float16)v;
+        const h4 hv = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, hv), rs, item_off + s_off[0],
+                                              0, 0);
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t off = ok[i] ? item_off + s_off[i] : kOob;
+      if (F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[i]), rs, off, 0, 0);
+      } else {
+        const _Float16 hv = (_Float16)v[i];
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, hv), rs, off, 0, 0);
       }
     }
@@ -2058,10 +2099,13 @@ conv3x3_tail(NarrowArgs a) {
 
   // Item k of a run uses window rows k, k+1, k+2 (slots k % NR, ...), then
   // loads row k + NR into the slot of row k; one barrier per item (the tile
-  // is double-buffered).
+  // is double-buffered). Walking up, window row k is the conv's bottom tap
+  // row, so the slots enter the MFMAs in the opposite order; the MFMA order,
+  // and so every result bit, is the same both ways.
   int par = 0;  // tile buffer of the current item
   bool have_prev = false;
-  auto item = [&](Row& r0, const Row& r1, const Row& r2, int k) {
+  auto item = [&](const Row& r0, const Row& r1, const Row& r2, Row& reload, int k, auto rev_tag) {
+    constexpr bool REV = decltype(rev_tag)::value;
     store_item(par ^ 1, have_prev);
     f4 acc = {0, 0, 0, 0};
 #pragma unroll
@@ -2070,41 +2114,66 @@ conv3x3_tail(NarrowArgs a) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r1.v[kc], wb[1][kc], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(r2.v[kc], wb[2][kc], acc, 0, 0, 0);
     }
-    load_row(r0, k + NR);
+    load_row(reload, k + NR, rev_tag);
     *reinterpret_cast<f4*>(tile + par * TILE + twr) = acc;
     pn = n;
     ps = sg;
-    ph = h0 + k;
+    ph = REV ? h0 + len - 1 - k : h0 + k;
     have_prev = true;
     par ^= 1;
     lds_sync();
   };
 
   Row W[NR];
-  for (int it = begin; it < end;) {
-    decode(it);
-    const int len = min(end - it, a.H - h0);
-    setup_run();
+  auto run = [&](auto rev_tag) {
+    constexpr bool REV = decltype(rev_tag)::value;
 #pragma unroll
-    for (int j = 0; j < NR; ++j) load_row(W[j], j);
+    for (int j = 0; j < NR; ++j) load_row(W[j], j, rev_tag);
+    auto step = [&](auto j_tag, int k) {
+      constexpr int J = decltype(j_tag)::value;
+      if constexpr (REV)
+        item(W[(J + 2) % NR], W[(J + 1) % NR], W[J], W[J], k, rev_tag);
+      else
+        item(W[J], W[(J + 1) % NR], W[(J + 2) % NR], W[J], k, rev_tag);
+    };
     // Whole cycles of the slots, then the remainder as nested conditions (one
     // loop exit keeps the compiler's count of outstanding loads exact).
     int k = 0;
     for (; k + NR <= len; k += NR) {
-#pragma unroll
-      for (int j = 0; j < NR; ++j) item(W[j], W[(j + 1) % NR], W[(j + 2) % NR], k + j);
+      static_for<NR>([&](auto j_tag) { step(j_tag, k + decltype(j_tag)::value); });
     }
     auto rest = [&](auto self, auto j_tag) {
       constexpr int J = decltype(j_tag)::value;
       if constexpr (J < NR) {
         if (k + J < len) {
-          item(W[J], W[(J + 1) % NR], W[(J + 2) % NR], k + J);
+          step(j_tag, k + J);
           self(self, IntC<J + 1>{});
         }
       }
     };
     rest(rest, IntC<0>{});
-    it += len;
+  };
+
+  // Odd slots walk their item range backwards (rows upward, runs in reverse),
+  // so that the two rows a run boundary shares are read by both neighbouring
+  // workgroups (same XCD) near the same time, at both ends of the launch, and
+  // the second read hits L2.
+  const bool rev = (slot & 1) != 0;
+  if (!rev) {
+    for (int it = begin; it < end; it += len) {
+      decode(it);
+      len = min(end - it, a.H - h0);
+      setup_run();
+      run(IntC<0>{});
+    }
+  } else {
+    for (int it = end; it > begin; it -= len) {
+      decode(it - 1);
+      len = min(it - begin, h0 + 1);
+      h0 = h0 - len + 1;
+      setup_run();
+      run(IntC<1>{});
+    }
   }
   store_item(par ^ 1, have_prev);
 }
@@ -2666,7 +2735,8 @@ __global__ void __launch_bounds__(256) input_convert_vec(IoArgs a) {
     h8 v;
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = iolds[(8 * q + k) * kIoVecRow + x];
-    __builtin_nontemporal_store(v, reinterpret_cast<h8*>(dst + (int64_t)x * C + 8 * q));
+    // Plain stores: the first conv reads this tensor next, partly from the cache.
+    *reinterpret_cast<h8*>(dst + (int64_t)x * C + 8 * q) = v;
   }
 }
 
