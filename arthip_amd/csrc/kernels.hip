@@ -1297,15 +1297,19 @@ winograd_pipe(StripArgs a) {
 // Per run (one strip, output tile rows j0 .. j0+len-1; t tile row i covers t
 // rows 2(j0+i)-1 and 2(j0+i), i = 0 .. len), phase k (k = 0 .. len+4) ends with
 // the workgroup barrier:
-//   conv1 waves: fold t_{k-1} from V1'[(k-1)&1] into ring slot (k-1)&1
-//                (1 <= k <= len+1); transform t_k into V1'[k&1] (k <= len) and
-//                load the input rows of t_{k+1}
-//   conv2 waves: store output row k-5 from staging[(k-5)&1] (k >= 5); fold
-//                output row k-4 from V2'[k&1] into staging[k&1]
+//   conv1 waves: store output row k-5 from staging[(k-5)&1] with its
+//                residuals (k >= 5) and load the residuals of row k-4;
+//                transform t_k into V1'[k&1] (k <= len) and load the input
+//                rows of t_{k+1}; fold t_{k-1} from V1'[(k-1)&1] into ring
+//                slot (k-1)&1 (1 <= k <= len+1)
+//   conv2 waves: fold output row k-4 from V2'[k&1] into staging[k&1]
 //                (4 <= k <= len+3); read t_{k-2} from the ring and transform
 //                output row k-3 into V2'[(k-3)&1] (3 <= k <= len+2; at k = 2
 //                only the read)
-// Every buffer's writer and readers are a barrier apart.
+// Every buffer's writer and readers are a barrier apart. The store sits with
+// the conv1 waves: with the conv2 waves it made theirs the longer chain by
+// about a third of a phase (timestamps per section), and moved over it took
+// the 1080p launch from 240 to 226 us.
 struct BlockL {
   static constexpr int C = 64;
   static constexpr int PX = 2 * C;                // bytes per pixel
@@ -1435,6 +1439,57 @@ winograd_block(BlockArgs a) {
   const int tt = gtid >> 4;
   const int tq = gtid & 15;
 
+  // Store phase (run by the conv1 waves, which finish their phase well before
+  // the conv2 waves): thread handles 16-byte group sg of pixel sx in both rows
+  // of the output row pair that left the conv2 fold last phase.
+  _Float16* const stg = blds + L::STG;
+  const int sx = gtid >> 3;
+  const int sg = gtid & 7;
+  const int sr0 = StripStage<2>::at(0, sx, sg);
+  const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
+  const int n_rec = (int)(rb32 + 32 * PX);
+  h8 skr[2][2];
+  // Buffer resources over output row pair o's first pixel of the strip, from
+  // the run's first row pair (byte offset of o: (o - j0) * 2 row_bytes). Lane
+  // offsets past the strip or the right edge, of the second row past the
+  // bottom, or of a phase with nothing to store are out of range: dropped
+  // stores, zero loads.
+  int64_t run_pix = 0;
+  uint32_t lane_off = kOob;
+  auto row_rsrc = [&](const void* base, int o) {
+    const char* p = reinterpret_cast<const char*>(base) + run_pix * PX +
+                    (int64_t)(o - j0) * (2 * row_bytes);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, n_rec, 0x00020000);
+  };
+  auto st_off = [&](bool live, int o, int r) -> uint32_t {
+    const bool ok = live && (r == 0 || 2 * o + 1 < a.H);  // uniform
+    return ok ? lane_off + (uint32_t)r * rb32 : kOob;
+  };
+  auto load_skips = [&](bool live, int o) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) skr[k][r] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < NSKIP; ++k) {
+      const __amdgpu_buffer_rsrc_t rs = row_rsrc(k == 0 ? a.skip0 : a.skip1, o);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        skr[k][r] = __builtin_bit_cast(
+            h8, __builtin_amdgcn_raw_buffer_load_b128(rs, st_off(live, o, r), 0, kNonTemporal));
+    }
+  };
+  auto store_row = [&](bool live, int o, int SB) {
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(a.out, o);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      h8 v = act8<ACT2>(*reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C));
+      if (NSKIP > 0) v += skr[0][r];
+      if (NSKIP > 1) v += skr[1][r];
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs, st_off(live, o, r), 0,
+                                             kNonTemporal);
+    }
+  };
   if (wave < 4) {
     // ---------------- conv1: in -> t ----------------------------------------
     h8 u[16][2];
@@ -1493,6 +1548,11 @@ winograd_block(BlockArgs a) {
       constexpr int P = decltype(par_tag)::value;  // k & 1
       h2(&top)[16] = P ? B : A;
       h2(&bot)[16] = P ? A : B;
+      // Output row k-5 leaves staging (k-5)&1 = P^1 (the conv2 fold of the
+      // last phase); its residuals were loaded last phase. Then the residuals
+      // of row k-4 (folded by conv2 this phase, stored next phase).
+      store_row(k >= 5, j0 + k - 5, P ^ 1);
+      load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
       // Transform first, fold second: the conv2 wave on the same SIMD folds
       // first, so one wave's VALU transform overlaps the other's MFMA chain
       // (and the next input rows are requested earlier).
@@ -1539,6 +1599,8 @@ winograd_block(BlockArgs a) {
         const int tc0 = L::OPX * s - 1 + 2 * tcol;
         cm0 = (tc0 >= 0 && tc0 < a.W) ? ~0u : 0u;
         cm1 = (tc0 + 1 < a.W) ? ~0u : 0u;
+        run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
+        lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
       }
       // t_0 needs padded rows 2 j0 - 1 .. 2 j0 + 2.
       load2(A, 2 * j0 - 1);
@@ -1564,7 +1626,6 @@ winograd_block(BlockArgs a) {
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) vr[kc] = blds + L::V2 + StripLds<2>::at(tcol, 32 * kc + 8 * kq);
   const _Float16* const ring = blds + L::RING;
-  _Float16* const stg = blds + L::STG;
   // Ring pixels of this task's patch: 2 tt .. 2 tt + 3 (tile 15 is not an
   // output of the strip; it reads tile 14's patch).
   // Row 0 addresses of the four pixels; row 1 and the slot are immediate
@@ -1586,62 +1647,11 @@ winograd_block(BlockArgs a) {
       }
   };
   const int sw0 = StripStage<2>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
-  // Store phase: thread handles 16-byte group sg of pixel sx in both rows.
-  const int sx = gtid >> 3;
-  const int sg = gtid & 7;
-  const int sr0 = StripStage<2>::at(0, sx, sg);
-  const uint32_t s_lane = (uint32_t)(sx * C + sg * 8) * 2;
-  const int n_rec = (int)(rb32 + 32 * PX);
-  h8 skr[2][2];
-  // Buffer resources over output row pair o's first pixel of the strip, from
-  // the run's first row pair (byte offset of o: (o - j0) * 2 row_bytes). Lane
-  // offsets past the strip or the right edge, of the second row past the
-  // bottom, or of a phase with nothing to store are out of range: dropped
-  // stores, zero loads.
-  int64_t run_pix = 0;
-  uint32_t lane_off = kOob;
-  auto row_rsrc = [&](const void* base, int o) {
-    const char* p = reinterpret_cast<const char*>(base) + run_pix * PX +
-                    (int64_t)(o - j0) * (2 * row_bytes);
-    return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, n_rec, 0x00020000);
-  };
-  auto st_off = [&](bool live, int o, int r) -> uint32_t {
-    const bool ok = live && (r == 0 || 2 * o + 1 < a.H);  // uniform
-    return ok ? lane_off + (uint32_t)r * rb32 : kOob;
-  };
-  auto load_skips = [&](bool live, int o) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-#pragma unroll
-      for (int r = 0; r < 2; ++r) skr[k][r] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int k = 0; k < NSKIP; ++k) {
-      const __amdgpu_buffer_rsrc_t rs = row_rsrc(k == 0 ? a.skip0 : a.skip1, o);
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-        skr[k][r] = __builtin_bit_cast(
-            h8, __builtin_amdgcn_raw_buffer_load_b128(rs, st_off(live, o, r), 0, kNonTemporal));
-    }
-  };
-  auto store_row = [&](bool live, int o, int SB) {
-    const __amdgpu_buffer_rsrc_t rs = row_rsrc(a.out, o);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      h8 v = act8<ACT2>(*reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C));
-      if (NSKIP > 0) v += skr[0][r];
-      if (NSKIP > 1) v += skr[1][r];
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs, st_off(live, o, r), 0,
-                                             kNonTemporal);
-    }
-  };
   h2 A[16], B[16];
   auto phase = [&](auto par_tag, int k, int len) {
     constexpr int P = decltype(par_tag)::value;  // k & 1
     h2(&cur)[16] = P ? B : A;
     h2(&nxt)[16] = P ? A : B;
-    // Output row k-5 leaves staging (k-5)&1 = P^1; its residuals were loaded
-    // last phase.
-    store_row(k >= 5, j0 + k - 5, P ^ 1);
     const bool fold = k >= 4 && k <= len + 3;
     if (fold) {
       f4 y00, y01, y10, y11;
@@ -1652,9 +1662,6 @@ winograd_block(BlockArgs a) {
       *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<kActNone>(y10);
       *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<kActNone>(y11);
     }
-    // Residual inputs of the row just folded (stored next phase); issued after
-    // the fold so that they are not live across it.
-    load_skips(fold, j0 + k - 4);
     if (k >= 2 && k <= len + 2) {
       // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is
       // the patch of output row k-3.
@@ -1666,8 +1673,6 @@ winograd_block(BlockArgs a) {
   for (int it = begin; it < end;) {
     decode(it);
     const int len = min(end - it, a.tiles_h - j0);
-    run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
-    lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
     block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
     it += len;
   }
