@@ -1298,7 +1298,8 @@ winograd_pipe(StripArgs a) {
 // rows 2(j0+i)-1 and 2(j0+i), i = 0 .. len), phase k (k = 0 .. len+4) ends with
 // the workgroup barrier:
 //   conv1 waves: store output row k-5 from staging[(k-5)&1] with its
-//                residuals (k >= 5) and load the residuals of row k-4;
+//                residuals (k >= 5) and load the residuals of row k-4 (up to
+//                one residual input; with two the conv2 waves do both);
 //                transform t_k into V1'[k&1] (k <= len) and load the input
 //                rows of t_{k+1}; fold t_{k-1} from V1'[(k-1)&1] into ring
 //                slot (k-1)&1 (1 <= k <= len+1)
@@ -1307,9 +1308,9 @@ winograd_pipe(StripArgs a) {
 //                output row k-3 into V2'[(k-3)&1] (3 <= k <= len+2; at k = 2
 //                only the read)
 // Every buffer's writer and readers are a barrier apart. The store sits with
-// the conv1 waves: with the conv2 waves it made theirs the longer chain by
-// about a third of a phase (timestamps per section), and moved over it took
-// the 1080p launch from 240 to 226 us.
+// the conv1 waves where it can: with the conv2 waves it made theirs the
+// longer chain by about a third of a phase (timestamps per section), and
+// moved over it took the 1080p one-residual launch from 240 to 226 us.
 struct BlockL {
   static constexpr int C = 64;
   static constexpr int PX = 2 * C;                // bytes per pixel
@@ -1439,9 +1440,12 @@ winograd_block(BlockArgs a) {
   const int tt = gtid >> 4;
   const int tq = gtid & 15;
 
-  // Store phase (run by the conv1 waves, which finish their phase well before
-  // the conv2 waves): thread handles 16-byte group sg of pixel sx in both rows
-  // of the output row pair that left the conv2 fold last phase.
+  // Store phase: thread handles 16-byte group sg of pixel sx in both rows of
+  // the output row pair that left the conv2 fold last phase. The conv1 waves
+  // run it with up to one residual input; with two, the residual registers
+  // held across the conv1 fold cost more than the store saves the conv2
+  // waves (1080p: 280 us against 260), so the conv2 waves keep it.
+  constexpr bool kConv1Stores = NSKIP < 2;
   _Float16* const stg = blds + L::STG;
   const int sx = gtid >> 3;
   const int sg = gtid & 7;
@@ -1551,8 +1555,10 @@ winograd_block(BlockArgs a) {
       // Output row k-5 leaves staging (k-5)&1 = P^1 (the conv2 fold of the
       // last phase); its residuals were loaded last phase. Then the residuals
       // of row k-4 (folded by conv2 this phase, stored next phase).
-      store_row(k >= 5, j0 + k - 5, P ^ 1);
-      load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
+      if constexpr (kConv1Stores) {
+        store_row(k >= 5, j0 + k - 5, P ^ 1);
+        load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
+      }
       // Transform first, fold second: the conv2 wave on the same SIMD folds
       // first, so one wave's VALU transform overlaps the other's MFMA chain
       // (and the next input rows are requested earlier).
@@ -1652,6 +1658,9 @@ winograd_block(BlockArgs a) {
     constexpr int P = decltype(par_tag)::value;  // k & 1
     h2(&cur)[16] = P ? B : A;
     h2(&nxt)[16] = P ? A : B;
+    // Output row k-5 leaves staging (k-5)&1 = P^1; its residuals were loaded
+    // last phase.
+    if constexpr (!kConv1Stores) store_row(k >= 5, j0 + k - 5, P ^ 1);
     const bool fold = k >= 4 && k <= len + 3;
     if (fold) {
       f4 y00, y01, y10, y11;
@@ -1662,6 +1671,9 @@ winograd_block(BlockArgs a) {
       *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<kActNone>(y10);
       *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<kActNone>(y11);
     }
+    // Residual inputs of the row just folded (stored next phase); issued after
+    // the fold so that they are not live across it.
+    if constexpr (!kConv1Stores) load_skips(fold, j0 + k - 4);
     if (k >= 2 && k <= len + 2) {
       // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is
       // the patch of output row k-3.
@@ -1673,6 +1685,8 @@ winograd_block(BlockArgs a) {
   for (int it = begin; it < end;) {
     decode(it);
     const int len = min(end - it, a.tiles_h - j0);
+    run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
+    lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
     block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
     it += len;
   }
