@@ -29,7 +29,7 @@ Extra objects in the line:
                 buffer, what streaming code reaches on this device.
   cpu_baseline  the CPU oracle (oracle/, plain C + OpenMP, fp32 math with fp16
                 storage between nodes) on a bounded band of the same frame on the
-                host's cores (2 warm-up runs, median of 3 timed runs), scaled to
+                host's cores (2 warm-up runs, median of 5 timed runs), scaled to
                 frames/s; with the thread count used, the physical cores and the
                 CPU model.
 """
@@ -66,8 +66,8 @@ def parse():
     p.add_argument("--batch", type=int, default=1)
     p.add_argument("--cpu-rows", type=int, default=-1,
                    help="rows of the frame in the CPU baseline sample (0 disables it; default: "
-                        "about 3 s of CPU work per run, 5 runs: r8f64 120, shipped_like 80, "
-                        "r16f96 24, single64 and c4f32 the whole frame)")
+                        "about 2-3 s of CPU work per run, 2 warm-up and 5 timed runs: r8f64 80, "
+                        "shipped_like 56, r16f96 16, single64 and c4f32 the whole frame)")
     p.add_argument("--no-profile", action="store_true",
                    help="skip the per-launch event timing (roofline becomes null)")
     p.add_argument("--host-path", type=int, default=0, metavar="STREAMS",
@@ -135,7 +135,7 @@ def host_cpu() -> tuple[str, int]:
 
 def cpu_baseline(spec, x_full, rows: int) -> dict | None:
     """Times the C oracle on a band of `rows` input rows (full width): two
-    warm-up runs, then the median of three timed runs."""
+    warm-up runs, then the median of five timed runs."""
     if rows <= 0:
         return None
     import statistics
@@ -150,7 +150,7 @@ def cpu_baseline(spec, x_full, rows: int) -> dict | None:
     for _ in range(2):
         run_model(spec.model, band)
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         run_model(spec.model, band)
         times.append(time.perf_counter() - t0)
@@ -166,7 +166,7 @@ def cpu_baseline(spec, x_full, rows: int) -> dict | None:
         "kind": "port",
         "sample": (f"{spec.name} on a {rows}x{x_full.shape[3]} row band of the "
                    f"{x_full.shape[2]}x{x_full.shape[3]} frame ({frac:.1%} of a frame); "
-                   f"2 warm-up runs, median of 3 timed runs ({', '.join(f'{t:.2f}' for t in times)} s); "
+                   f"2 warm-up runs, median of 5 timed runs ({', '.join(f'{t:.2f}' for t in times)} s); "
                    f"C oracle, fp32 math + fp16 storage per node, OpenMP on {threads} threads; "
                    f"frames/s = band fraction / time"),
     }
@@ -558,7 +558,7 @@ def main() -> int:
 
     rows = args.cpu_rows
     if rows < 0:
-        rows = {"r8f64": 120, "shipped_like": 80, "r16f96": 24}.get(args.model, h)
+        rows = {"r8f64": 80, "shipped_like": 56, "r16f96": 16}.get(args.model, h)
     cpu = cpu_baseline(spec, x_host, min(rows, h)) if rows else None
 
     tflops_direct = work["flops_direct"] * fps / n / 1e12
