@@ -1949,28 +1949,30 @@ conv3x3_narrow(NarrowArgs a) {
 // wave's 16 pixels x; dy and the chunks accumulate in the MFMA, so a wave
 // issues 3 * KC MFMAs per item instead of 9 * KC. The conv output is
 // out[x][n] = D[x][(0,n)] + D[x+1][(1,n)] + D[x+2][(2,n)] (+ bias), summed in
-// the store phase from an fp32 tile [16 columns][64 pixels] in LDS.
+// the store phase from an fp32 tile [16 columns][128 pixels] in LDS.
 //
-// A workgroup walks down a segment of TAIL_SEG = 62 output pixels (one output
-// row per item): its four waves cover the segment's 64 padded input columns,
-// halo included. The A fragments (16 pixels x 32 channels, 16 bytes per lane)
+// A workgroup walks down a segment of TAIL_SEG = 126 output pixels (one output
+// row per item): its eight waves cover the segment's 128 padded input columns,
+// halo included (four waves and 62-pixel segments: 65.3 us at 1080p against
+// 63.4; sixteen waves: no better). The A fragments (16 pixels x 32 channels, 16 bytes per lane)
 // come straight from HBM into a register window of TAIL_ROWS input rows: each
 // item consumes three and loads one TAIL_ROWS - 3 rows ahead. (Through an LDS
 // ring filled by global_load_lds the same conv ran at 95 us at 1080p, held
 // back by the DMA issue and LDS bank conflicts.)
 constexpr int TAIL_ROWS = 6;
-// Floats per D tile row: the segment's 64 pixels padded to 18 bank quads, so
-// that the 16 lanes a ds_write_b128 serves per cycle (columns t..t+7 and two
-// adjacent 4-pixel groups) land on 16 distinct quads. Rows of 64 floats put
-// every column on the same quads: 8-way conflicts on each write.
-constexpr int TAIL_TW = 72;
-constexpr int TAIL_SEG = 62;
+constexpr int TAIL_WAVES = 8;                  // 16 input columns each
+constexpr int TAIL_SEG = 16 * TAIL_WAVES - 2;  // output pixels per segment
+// Floats per D tile row: the segment's input columns padded by 8 (two bank
+// quads), so that the 16 lanes a ds_write_b128 serves per cycle (columns
+// t..t+7 and two adjacent 4-pixel groups) land on 16 distinct quads. Rows of
+// 64 floats put every column on the same quads: 8-way conflicts on each write.
+constexpr int TAIL_TW = 16 * TAIL_WAVES + 8;
 
-// Four workgroups per CU for C <= 64 (two for C = 96, whose row window needs
+// Four waves per SIMD for C <= 64 (two for C = 96, whose row window needs
 // more than 128 VGPRs): at 1080p 64 -> 4 + DepthToSpace, 81 us with two, 70 us
-// with four.
+// with four (measured with four-wave workgroups).
 template <int KC, bool F32>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * TAIL_WAVES)
     __attribute__((amdgpu_waves_per_eu(KC == 3 ? 2 : 4, KC == 3 ? 2 : 4)))
 conv3x3_tail(NarrowArgs a) {
   constexpr int C = 32 * KC;
@@ -3165,13 +3167,15 @@ hipError_t launch_narrow_kc(const NarrowArgs& a, bool f32, hipStream_t s) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
+  const int threads = rows ? 64 * TAIL_WAVES : 256;
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, lds) != hipSuccess || occ < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, lds) != hipSuccess ||
+      occ < 1)
     occ = 1;
   int64_t grid = (int64_t)cu_count() * occ;
   if (grid > a.n_items) grid = a.n_items;
   grid = (grid + 7) / 8 * 8;
-  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(256), lds, s, a);
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(threads), lds, s, a);
   return hipGetLastError();
 }
 
