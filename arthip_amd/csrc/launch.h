@@ -11,6 +11,11 @@
 
 namespace arthip {
 
+// Compute units of the current device (queried once; 256 when unknown).
+int cu_count();
+// Multiply-shift constants for dividing uniform values < 2^31 by d on the GPU.
+FastDiv make_fastdiv(uint32_t d);
+
 // Largest channel counts the register-resident Winograd kernel is built for.
 int winograd_max_kc();  // input channels <= 32 * winograd_max_kc()
 int winograd_max_m();   // output channels

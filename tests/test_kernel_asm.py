@@ -4,11 +4,11 @@ Mirrors the reference's kernel memory-ordering gate (tests/correctness/
 test_kernel.py): an `s_barrier` orders control flow but does not retire
 outstanding LDS stores, so a wave could pass a barrier with its stores still in
 flight and another wave read stale shared memory (the corruption the reference's
-NOTES.md describes). Every barrier in kernels.hip goes through `lds_sync`, which
-emits `s_waitcnt lgkmcnt(0)` itself instead of relying on the compiler's waitcnt
-pass. Checked two ways:
+NOTES.md describes). Every barrier in the HIP sources (kernels.hip, block.hip)
+goes through `lds_sync` (wino_dev.h), which emits `s_waitcnt lgkmcnt(0)` itself
+instead of relying on the compiler's waitcnt pass. Checked two ways:
 - in the source: `__syncthreads` appears only inside `lds_sync`;
-- in the gfx950 assembly hipcc emits for kernels.hip: in every kernel, walking
+- in the gfx950 assembly hipcc emits for each HIP source: in every kernel, walking
   back from each `s_barrier` inside its basic block, an `s_waitcnt lgkmcnt(0)`
   comes before any LDS instruction (the compiler may schedule ALU work between
   the drain and the barrier, which is harmless).
@@ -26,6 +26,8 @@ import pytest
 
 CSRC = Path(__file__).resolve().parents[1] / "arthip_amd" / "csrc"
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+HIP_SOURCES = sorted(p.name for p in CSRC.glob("*.hip"))
+DEVICE_SOURCES = HIP_SOURCES + ["wino_dev.h"]
 
 
 def _strip_comments(text: str) -> str:
@@ -34,27 +36,38 @@ def _strip_comments(text: str) -> str:
 
 
 def test_barriers_only_through_lds_sync():
-    src = _strip_comments((CSRC / "kernels.hip").read_text())
-    m = re.search(r"void lds_sync\(\)\s*\{(.*?)\n\}", src, flags=re.S)
-    assert m, "lds_sync not found"
-    body = m.group(1)
-    assert "lgkmcnt(0)" in body and "__syncthreads" in body
-    rest = src[:m.start()] + src[m.end():]
-    assert "__syncthreads" not in rest, "a barrier outside lds_sync"
-    assert "s_barrier" not in rest, "a raw s_barrier outside lds_sync"
+    assert "kernels.hip" in HIP_SOURCES and "block.hip" in HIP_SOURCES
+    found = 0
+    for name in DEVICE_SOURCES:
+        src = _strip_comments((CSRC / name).read_text())
+        m = re.search(r"void lds_sync\(\)\s*\{(.*?)\n\}", src, flags=re.S)
+        if m:
+            found += 1
+            body = m.group(1)
+            assert "lgkmcnt(0)" in body and "__syncthreads" in body
+            src = src[:m.start()] + src[m.end():]
+        assert "__syncthreads" not in src, f"{name}: a barrier outside lds_sync"
+        assert "s_barrier" not in src, f"{name}: a raw s_barrier outside lds_sync"
+    assert found == 1, f"lds_sync defined {found} times"
 
 
 @pytest.fixture(scope="session")
 def kernel_asm(tmp_path_factory) -> str:
+    """The gfx950 assembly of every HIP source, concatenated."""
     if not Path(HIPCC).exists():
         pytest.skip("hipcc not available")
-    src = CSRC / "kernels.hip"
-    digest = hashlib.sha1(src.read_bytes()).hexdigest()[:12]
-    out = tmp_path_factory.mktemp("asm") / f"kernels_{digest}.s"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
-           "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S", "-o", str(out), str(src)]
-    subprocess.run(cmd, check=True, cwd=CSRC, capture_output=True)
-    return out.read_text()
+    tmp = tmp_path_factory.mktemp("asm")
+    text = []
+    for name in HIP_SOURCES:
+        src = CSRC / name
+        digest = hashlib.sha1(src.read_bytes()).hexdigest()[:12]
+        out = tmp / f"{src.stem}_{digest}.s"
+        cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+               "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S", "-o", str(out),
+               str(src)]
+        subprocess.run(cmd, check=True, cwd=CSRC, capture_output=True)
+        text.append(out.read_text())
+    return "\n".join(text)
 
 
 def _kernels(asm: str):
