@@ -265,6 +265,34 @@ def test_shipped_model_full_1920_real_image():
           "(reference vs ONNX Runtime CPU: 0.00134)" % (worst[True], worst[False]))
 
 
+def test_r8f64_8k_frame_past_2gib_activations():
+    """One 7680x4320 frame: each padded 64-channel activation is 4.25 GB, past the
+    32-bit buffer-resource range of the fused block and the row-packed tail, so
+    the engine runs every conv unfused (winograd_pipe / winograd_strip, the
+    general tail). Finite, bit-stable, and four windows (two corners, the middle,
+    the right edge) against the oracle with an 18-pixel margin."""
+    spec = models.r8f64(seed=0)
+    x = models.synthetic_input((1, 1, 4320, 7680), seed=3)
+    with Engine(0) as e:
+        e.build(spec)
+        e.set_profiling(True)
+        got = e.run(x)
+        steps = [name for name, _, _ in e.profile_read()]
+        e.set_profiling(False)
+        again = e.run(x)
+        plan = e.describe()
+    assert steps and not any("block" in s for s in steps), steps
+    assert "18 launches" in plan, plan
+    assert got.shape == (1, 1, 8640, 15360) and np.isfinite(got).all()
+    np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16))
+    got = got.astype(np.float32)
+    for r0, r1, c0, c1 in ((0, 24, 0, 96), (2144, 2168, 3808, 3904), (4296, 4320, 7584, 7680),
+                           (1200, 1224, 7632, 7680)):
+        s, floor = _band_check(got, spec, x, r0, r1, 18, c0, c1)
+        print("r8f64 8k window", (r0, r1, c0, c1), s, "floor", floor)
+        assert s["rel_rms"] <= max(FLOOR_RATIO * floor["rel_rms"], 2e-3), (s, floor)
+
+
 @pytest.mark.parametrize("builder,hw", [(models.c4f32, (36, 52)), (models.r8f64, (24, 40)),
                                         (models.shipped_like, (20, 36))])
 def test_fp32_model_runs_the_fp16_network(builder, hw):
