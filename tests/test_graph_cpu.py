@@ -40,6 +40,16 @@ def test_broadcast_fails_shape_propagation(fixtures):
         e.output_shape((1, 4, 16, 16))
 
 
+@pytest.mark.parametrize("shape", [(1, 1, 0, 16), (1, 1, 16, 0), (0, 1, 16, 16)])
+def test_empty_frames_fail_shape_propagation(shape):
+    """A frame with a zero dimension is refused before anything is planned or
+    launched; the smallest frame, 1x1, propagates."""
+    e = Engine(0).build(models.r8f64())
+    with pytest.raises(EngineError, match="shape propagation failed"):
+        e.output_shape(shape)
+    assert e.output_shape((1, 1, 1, 1)) == (1, 1, 2, 2)
+
+
 def test_channel_mismatch_fails_shape_propagation(fixtures):
     e = Engine(0).build(fixtures.get("conv_c4m8").model)
     with pytest.raises(EngineError):
