@@ -84,7 +84,7 @@ struct StripArgs {
   FastDiv fd_tiles_h, fd_strips;
 };
 
-// Fused residual block of two 64 -> 64 convs (winograd_block in kernels.hip):
+// Fused residual block of two 64 -> 64 convs (winograd_block in block.hip):
 // out = act2(conv2(act1(conv1(in) + bias1)) + bias2) + skip0 + skip1, every
 // tensor padded NHWC fp16 with the input's geometry. Work items are 1 output
 // tile row x 15 tiles (a 30-pixel strip), ordered (n, strip, tile row) with the

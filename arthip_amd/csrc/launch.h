@@ -1,5 +1,6 @@
-// Host launchers for the gfx950 kernels (defined in kernels.hip). All launch
-// on the given stream and return the launch status.
+// Host launchers for the gfx950 kernels (defined in kernels.hip; the fused
+// block's launcher in block.hip). All launch on the given stream and return the
+// launch status.
 #pragma once
 
 #include <hip/hip_runtime.h>
