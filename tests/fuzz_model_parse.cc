@@ -1,5 +1,7 @@
 // Mutation fuzzer for the engine's model front end (onnx.cc ParseModel,
-// graph.cc BuildGraph and PropagateShapes), built by tests/test_fuzz_cpu.py
+// graph.cc BuildGraph and PropagateShapes) and the EP's partition (ep.cc
+// EpPartition, EpRunBoundary, EpNodeKeys, EpRunModel and a build of each claimed
+// run's model), built by tests/test_fuzz_cpu.py
 // with AddressSanitizer and UndefinedBehaviorSanitizer on the host. Every
 // mutated model must be accepted or refused with an error: a sanitizer report
 // or a crash fails the run.
@@ -15,6 +17,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "ep.h"
 #include "graph.h"
 #include "onnx.h"
 
@@ -79,7 +82,7 @@ int main(int argc, char** argv) {
   }
   Rng rng{std::strtoull(argv[1], nullptr, 10)};
   const long iters = std::strtol(argv[2], nullptr, 10);
-  long parsed = 0, built = 0, shaped = 0, thrown = 0;
+  long parsed = 0, built = 0, shaped = 0, claimed = 0, thrown = 0;
   for (int f = 3; f < argc; ++f) {
     std::ifstream in(argv[f], std::ios::binary);
     const std::vector<unsigned char> good((std::istreambuf_iterator<char>(in)), {});
@@ -94,6 +97,18 @@ int main(int argc, char** argv) {
         std::string err;
         if (!arthip::onnx::ParseModel(b.data(), b.size(), m, err)) continue;
         ++parsed;
+        std::vector<arthip::EpRun> runs;
+        if (arthip::EpPartition(m, runs, err)) {
+          for (const arthip::EpRun& run : runs) {
+            std::vector<std::string> acts, consts, outs, keys;
+            arthip::onnx::Model sub;
+            arthip::Graph sg;
+            if (arthip::EpRunBoundary(m, run.nodes, acts, consts, outs, err) &&
+                arthip::EpNodeKeys(m, run.nodes, keys, err) &&
+                arthip::EpRunModel(m, run.nodes, sub, err) && arthip::BuildGraph(sub, sg, err))
+              ++claimed;
+          }
+        }
         arthip::Graph g;
         if (!arthip::BuildGraph(m, g, err)) continue;
         ++built;
@@ -105,6 +120,7 @@ int main(int argc, char** argv) {
       }
     }
   }
-  std::printf("parsed %ld built %ld shaped %ld thrown %ld\n", parsed, built, shaped, thrown);
+  std::printf("parsed %ld built %ld shaped %ld claimed %ld thrown %ld\n", parsed, built, shaped,
+              claimed, thrown);
   return 0;
 }

@@ -3,7 +3,8 @@ and UndefinedBehaviorSanitizer (host code only, built with g++).
 
 The VapourSynth filter loads user-supplied model files and the ONNX Runtime EP
 hands over serialized graphs, both decoded by the library's own protobuf reader
-(onnx.cc) and graph builder (graph.cc). tests/fuzz_model_parse.cc truncates,
+(onnx.cc), graph builder (graph.cc) and the EP's partition (ep.cc).
+tests/fuzz_model_parse.cc truncates,
 bit-flips, splices and pads valid models with oversized varints; every mutant
 must be decoded or refused with an error. A sanitizer report (out-of-bounds
 read, overflow, use of uninitialised memory) aborts the run and fails the test.
@@ -32,6 +33,7 @@ def fuzzer(tmp_path_factory):
     cmd = [gxx, "-std=c++17", "-O1", "-g", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
            "-I", str(CSRC), "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
            str(HERE / "fuzz_model_parse.cc"), str(CSRC / "onnx.cc"), str(CSRC / "graph.cc"),
+           str(CSRC / "ep.cc"),
            "-o", str(exe)]
     subprocess.run(cmd, check=True, capture_output=True)
     return exe
