@@ -32,6 +32,9 @@ Extra objects in the line:
                 host's cores (2 warm-up runs, median of 5 timed runs), scaled to
                 frames/s; with the thread count used, the physical cores and the
                 CPU model.
+  cpu_library   the same band through torch's CPU conv2d (oneDNN) in fp32 on all
+                host threads: what an optimized CPU library reaches on this model
+                (ONNX Runtime is not installed), for scale beside the oracle.
 """
 
 from __future__ import annotations
@@ -169,6 +172,76 @@ def cpu_baseline(spec, x_full, rows: int) -> dict | None:
                    f"2 warm-up runs, median of 5 timed runs ({', '.join(f'{t:.2f}' for t in times)} s); "
                    f"C oracle, fp32 math + fp16 storage per node, OpenMP on {threads} threads; "
                    f"frames/s = band fraction / time"),
+    }
+
+
+def cpu_library(spec, x_full, rows: int) -> dict | None:
+    """The same band through torch's CPU conv2d (oneDNN) in fp32, all host
+    threads: what an optimized CPU library reaches on this model, for scale
+    beside the oracle figure (ONNX Runtime, whose CPU EP would be the reference's
+    own baseline, is not installed). Two warm-up runs, the median of five."""
+    if rows <= 0:
+        return None
+    import statistics
+
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from arthip_amd import onnx_proto as op
+
+    g = spec.model.graph
+    consts = {t.name: torch.from_numpy(t.to_numpy().astype(np.float32)) for t in g.initializers}
+    inp = next(v for v in g.inputs if v.name not in consts)
+    band = torch.from_numpy(np.ascontiguousarray(x_full[:, :, :rows, :]).astype(np.float32))
+
+    def run():
+        vals = {inp.name: band}
+        for n in g.nodes:
+            a, t = n.inputs, n.op_type
+            if t == "Conv":
+                b = consts[a[2]] if len(a) > 2 and a[2] else None
+                y = F.conv2d(vals[a[0]], consts[a[1]], b, padding=1)
+            elif t == "Relu":
+                y = torch.relu(vals[a[0]])
+            elif t == "Sigmoid":
+                y = torch.sigmoid(vals[a[0]])
+            elif t in ("Add", "Mul"):
+                u, v = (vals[k] if k in vals else consts[k] for k in a[:2])
+                y = u + v if t == "Add" else u * v
+            elif t == "Clip":
+                lo = consts[a[1]].item() if len(a) > 1 and a[1] else None
+                hi = consts[a[2]].item() if len(a) > 2 and a[2] else None
+                y = torch.clamp(vals[a[0]], lo, hi)
+            elif t == "DepthToSpace":
+                bs = int(n.attr("blocksize"))
+                x = vals[a[0]]
+                N, C, H, W = x.shape
+                y = (x.reshape(N, bs, bs, C // (bs * bs), H, W).permute(0, 3, 4, 1, 5, 2)
+                     .reshape(N, C // (bs * bs), H * bs, W * bs))
+            elif t == "Cast":
+                y = vals[a[0]]
+            else:
+                raise NotImplementedError(t)
+            vals[n.outputs[0]] = y
+        return vals[g.outputs[0].name]
+
+    with torch.inference_mode():
+        for _ in range(2):
+            run()
+        times = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+    dt = statistics.median(times)
+    frac = rows / x_full.shape[2]
+    return {
+        "value": round(frac / dt, 4),
+        "unit": "frames/s",
+        "threads": torch.get_num_threads(),
+        "what": (f"torch {torch.__version__} CPU conv2d (oneDNN), fp32 throughout, on the same "
+                 f"{rows}-row band; median of 5 runs ({', '.join(f'{t:.3f}' for t in times)} s)"),
     }
 
 
@@ -560,6 +633,7 @@ def main() -> int:
     if rows < 0:
         rows = {"r8f64": 80, "shipped_like": 56, "r16f96": 16}.get(args.model, h)
     cpu = cpu_baseline(spec, x_host, min(rows, h)) if rows else None
+    cpu_lib = cpu_library(spec, x_host, min(rows, h)) if rows else None
 
     tflops_direct = work["flops_direct"] * fps / n / 1e12
     line = {
@@ -592,6 +666,7 @@ def main() -> int:
         "wall_s": round(wall, 3),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_library": cpu_lib,
     }
     if os.environ.get("ARTHIP_BENCH_STEPS_REPORT"):
         line["steps_report"] = steps_report
