@@ -175,28 +175,21 @@ def cpu_baseline(spec, x_full, rows: int) -> dict | None:
     }
 
 
-def cpu_library(spec, x_full, rows: int) -> dict | None:
-    """The same band through torch's CPU conv2d (oneDNN) in fp32, all host
-    threads: what an optimized CPU library reaches on this model, for scale
-    beside the oracle figure (ONNX Runtime, whose CPU EP would be the reference's
-    own baseline, is not installed). Two warm-up runs, the median of five."""
-    if rows <= 0:
-        return None
-    import statistics
-
+def torch_cpu_runner(model, x):
+    """A callable that evaluates `model` (an arthip_amd.onnx_proto Model of the
+    conv-chain ops) on NCHW input x with torch's CPU kernels, fp32 throughout,
+    and returns the output tensor."""
     import numpy as np
     import torch
     import torch.nn.functional as F
 
-    from arthip_amd import onnx_proto as op
-
-    g = spec.model.graph
+    g = model.graph
     consts = {t.name: torch.from_numpy(t.to_numpy().astype(np.float32)) for t in g.initializers}
     inp = next(v for v in g.inputs if v.name not in consts)
-    band = torch.from_numpy(np.ascontiguousarray(x_full[:, :, :rows, :]).astype(np.float32))
+    xin = torch.from_numpy(np.ascontiguousarray(x).astype(np.float32))
 
     def run():
-        vals = {inp.name: band}
+        vals = {inp.name: xin}
         for n in g.nodes:
             a, t = n.inputs, n.op_type
             if t == "Conv":
@@ -215,9 +208,9 @@ def cpu_library(spec, x_full, rows: int) -> dict | None:
                 y = torch.clamp(vals[a[0]], lo, hi)
             elif t == "DepthToSpace":
                 bs = int(n.attr("blocksize"))
-                x = vals[a[0]]
-                N, C, H, W = x.shape
-                y = (x.reshape(N, bs, bs, C // (bs * bs), H, W).permute(0, 3, 4, 1, 5, 2)
+                v = vals[a[0]]
+                N, C, H, W = v.shape
+                y = (v.reshape(N, bs, bs, C // (bs * bs), H, W).permute(0, 3, 4, 1, 5, 2)
                      .reshape(N, C // (bs * bs), H * bs, W * bs))
             elif t == "Cast":
                 y = vals[a[0]]
@@ -226,6 +219,21 @@ def cpu_library(spec, x_full, rows: int) -> dict | None:
             vals[n.outputs[0]] = y
         return vals[g.outputs[0].name]
 
+    return run
+
+
+def cpu_library(spec, x_full, rows: int) -> dict | None:
+    """The same band through torch's CPU conv2d (oneDNN) in fp32, all host
+    threads: what an optimized CPU library reaches on this model, for scale
+    beside the oracle figure (ONNX Runtime, whose CPU EP would be the reference's
+    own baseline, is not installed). Two warm-up runs, the median of five."""
+    if rows <= 0:
+        return None
+    import statistics
+
+    import torch
+
+    run = torch_cpu_runner(spec.model, x_full[:, :, :rows, :])
     with torch.inference_mode():
         for _ in range(2):
             run()
