@@ -196,6 +196,12 @@ winograd_block(BlockArgs a) {
   // held across the conv1 fold cost more than the store saves the conv2
   // waves (1080p: 280 us against 260), so the conv2 waves keep it.
   constexpr bool kConv1Stores = NSKIP < 2;
+  // With act1 ReLU or none, conv1 runs on U1' / 4 and bias1 / 4 and the ring
+  // holds t / 4: the power-of-two scale commutes with the activation and with
+  // every fp16 and fp32 rounding (outside the subnormal range), so conv2's
+  // transform of the ring equals the 1/4-scaled transform of t and drops its
+  // own 1/4 (16 of 64 packed ops per transform). SiLU does not commute.
+  constexpr bool kQuarterT = ACT1 != kActSilu;
   _Float16* const stg = blds + L::STG;
   const int sx = gtid >> 3;
   const int sg = gtid & 7;
@@ -254,7 +260,14 @@ winograd_block(BlockArgs a) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) u[p][kc] = up[(p * 2 + kc) * 64];
     }
-    const f4 bias4 = *reinterpret_cast<const f4*>(a.bias1 + ch0);
+    f4 bias4 = *reinterpret_cast<const f4*>(a.bias1 + ch0);
+    if constexpr (kQuarterT) {
+#pragma unroll
+      for (int p = 0; p < 16; ++p)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) u[p][kc] *= (_Float16)0.25f;
+      bias4 *= 0.25f;
+    }
     _Float16* const vw = blds + L::V1 + StripLds<2>::at(tt, 4 * tq);
     const _Float16* vr[2];
 #pragma unroll
@@ -428,7 +441,7 @@ winograd_block(BlockArgs a) {
       // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is
       // the patch of output row k-3.
       ring_load2(nxt, P);
-      if (k >= 3) v_transform<WPS>(vw + (P ^ 1) * VBUF, cur, nxt);
+      if (k >= 3) v_transform<WPS, !kQuarterT>(vw + (P ^ 1) * VBUF, cur, nxt);
     }
     lds_sync();
   };

@@ -84,8 +84,9 @@ struct StripLds {
 constexpr int kNonTemporal = 2;
 
 // V' of one (tile, 4-channel) task from its 4x4 patch (rows 0-1 in top, 2-3
-// in bot), written to LDS at vw + position * WPS.
-template <int WPS>
+// in bot), written to LDS at vw + position * WPS. With kQuarter false the
+// column stage leaves out the 1/4 (for a patch whose values already carry it).
+template <int WPS, bool kQuarter = true>
 __device__ __forceinline__ void v_transform(_Float16* vw, const h2 (&top)[16],
                                             const h2 (&bot)[16]) {
   const h2 qp = {0.25f16, 0.25f16};
@@ -107,12 +108,19 @@ __device__ __forceinline__ void v_transform(_Float16* vw, const h2 (&top)[16],
     h2 o[4][2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const h2 n1 = t[i][1][e] * qn;
-      const h2 n2 = t[i][2][e] * qn;
-      o[0][e] = __builtin_elementwise_fma(t[i][0][e], qp, n2);
-      o[1][e] = __builtin_elementwise_fma(t[i][1][e], qp, -n2);
-      o[2][e] = __builtin_elementwise_fma(t[i][2][e], qp, n1);
-      o[3][e] = __builtin_elementwise_fma(t[i][3][e], qp, n1);
+      if constexpr (kQuarter) {
+        const h2 n1 = t[i][1][e] * qn;
+        const h2 n2 = t[i][2][e] * qn;
+        o[0][e] = __builtin_elementwise_fma(t[i][0][e], qp, n2);
+        o[1][e] = __builtin_elementwise_fma(t[i][1][e], qp, -n2);
+        o[2][e] = __builtin_elementwise_fma(t[i][2][e], qp, n1);
+        o[3][e] = __builtin_elementwise_fma(t[i][3][e], qp, n1);
+      } else {
+        o[0][e] = pk_sub(t[i][0][e], t[i][2][e]);
+        o[1][e] = t[i][1][e] + t[i][2][e];
+        o[2][e] = pk_sub(t[i][2][e], t[i][1][e]);
+        o[3][e] = pk_sub(t[i][3][e], t[i][1][e]);
+      }
     }
     _Float16* row = vw + (4 * i) * WPS;
 #pragma unroll
