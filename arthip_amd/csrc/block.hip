@@ -148,7 +148,7 @@ __device__ __forceinline__ void block_phases(int len, F&& ph) {
   }
 }
 
-template <int ACT1, int ACT2, int NSKIP>
+template <int ACT1, int ACT2, int NSKIP, bool kCachedOut>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 winograd_block(BlockArgs a) {
   using L = BlockL;
@@ -247,7 +247,7 @@ winograd_block(BlockArgs a) {
       if (NSKIP > 0) v += skr[0][r];
       if (NSKIP > 1) v += skr[1][r];
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), rs, st_off(live, o, r), 0,
-                                             kNonTemporal);
+                                             kCachedOut ? 0 : kNonTemporal);
     }
   };
   if (wave < 4) {
@@ -461,13 +461,18 @@ winograd_block(BlockArgs a) {
 
 using BlockKernel = void (*)(BlockArgs);
 
-template <int ACT1>
+template <int ACT1, bool kCachedOut>
 BlockKernel block_kernel_for(int nskip) {
   switch (nskip) {
-    case 0: return winograd_block<ACT1, kActNone, 0>;
-    case 1: return winograd_block<ACT1, kActNone, 1>;
-    default: return winograd_block<ACT1, kActNone, 2>;
+    case 0: return winograd_block<ACT1, kActNone, 0, kCachedOut>;
+    case 1: return winograd_block<ACT1, kActNone, 1, kCachedOut>;
+    default: return winograd_block<ACT1, kActNone, 2, kCachedOut>;
   }
+}
+
+template <int ACT1>
+BlockKernel block_kernel_for(int nskip, bool cached_out) {
+  return cached_out ? block_kernel_for<ACT1, true>(nskip) : block_kernel_for<ACT1, false>(nskip);
 }
 
 bool block_eligible(int C, int M, int act1, int act2, int64_t N, int64_t H, int64_t W) {
@@ -495,9 +500,10 @@ hipError_t launch_block(BlockArgs a, hipStream_t s) {
   a.n_items = (int32_t)items;
   a.fd_tiles_h = make_fastdiv((uint32_t)a.tiles_h);
   a.fd_strips = make_fastdiv((uint32_t)a.n_strips);
-  const BlockKernel fn = a.act1 == kActRelu   ? block_kernel_for<kActRelu>(nskip)
-                         : a.act1 == kActSilu ? block_kernel_for<kActSilu>(nskip)
-                                              : block_kernel_for<kActNone>(nskip);
+  const bool cached = a.cached_out != 0;
+  const BlockKernel fn = a.act1 == kActRelu   ? block_kernel_for<kActRelu>(nskip, cached)
+                         : a.act1 == kActSilu ? block_kernel_for<kActSilu>(nskip, cached)
+                                              : block_kernel_for<kActNone>(nskip, cached);
   const size_t lds = BlockL::lds_bytes();
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

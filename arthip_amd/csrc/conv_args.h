@@ -100,6 +100,9 @@ struct BlockArgs {
   uint16_t* out;
   int32_t N, H, W, Hp, Wp;
   int32_t act1, act2;
+  // 0: output stores carry the non-temporal hint; 1: plain stores, for an
+  // output that the next kernel reads while much of it is still cached.
+  int32_t cached_out;
   int32_t tiles_h, n_strips;
   int32_t n_items;  // N * n_strips * tiles_h
   FastDiv fd_tiles_h, fd_strips;

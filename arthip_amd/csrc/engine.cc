@@ -607,6 +607,33 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
     p.steps.push_back(st);
   }
 
+  // A block stores its output with plain stores (not non-temporal) when the
+  // next step is bound by HBM and the output fits the 256 MiB last-level
+  // cache (Infinity Cache) about once, so that this reader finds much of it
+  // still cached. HBM-bound readers: a conv writing the boundary output (the
+  // tail), a conv with residual inputs, and the elementwise and layout passes.
+  // Another block, or a conv without residual inputs into padded NHWC, is
+  // bound by its own arithmetic and gains nothing, while plain stores cost the
+  // writing block ~1-4 us. At 1080p (266 MB): R8F64's tail 64 -> 55 us, the
+  // shipped architecture's residual conv after its last block 167 -> 157 us,
+  // both frames ~0.2% faster. At 4K x 2 (2.1 GB) the tail slowed 483 -> 493 us.
+  constexpr int64_t kCachedOutMax = 320ll << 20;
+  auto hbm_bound = [](const Step& n) {
+    switch (n.kind) {
+      case StepKind::ConvBlock: return false;
+      case StepKind::ConvWinograd:
+      case StepKind::ConvDirect:
+        return n.epi.out_kind != kOutPadded || n.skip[0] != kNoBuffer;
+      default: return true;
+    }
+  };
+  for (size_t j = 0; j + 1 < p.steps.size(); ++j) {
+    Step& st = p.steps[j];
+    if (st.kind != StepKind::ConvBlock) continue;
+    const int64_t out_bytes = (int64_t)st.N * padded_rows(st.H) * padded_cols(st.W) * st.M * 2;
+    st.cached_out = out_bytes <= kCachedOutMax && hbm_bound(p.steps[j + 1]);
+  }
+
   p.in_bytes = static_cast<size_t>(in[0] * in[1] * in[2] * in[3]) * (graph_.input_fp32 ? 4 : 2);
   p.out_bytes = OutputBytesUnlocked(in);
   if (p.scratch) {
@@ -759,6 +786,7 @@ bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream
         a.N = st.N; a.H = st.H; a.W = st.W;
         a.act1 = st.epi.act;
         a.act2 = kActNone;
+        a.cached_out = st.cached_out ? 1 : 0;
         e = launch_block(a, s);
         break;
       }
@@ -876,6 +904,7 @@ std::string Engine::StepName(const Step& st) const {
       os << "winograd_block C64 M64" << acts[st.epi.act];
       for (int k = 0; k < 2; ++k)
         if (st.skip[k] != kNoBuffer) os << " +skip";
+      if (st.cached_out) os << " +cached_out";
       break;
     case StepKind::Eltwise: os << "eltwise op" << st.elt_op << (st.binary ? " binary" : ""); break;
     case StepKind::DepthToSpace: os << "depth_to_space b" << st.dts_b; break;

@@ -71,6 +71,7 @@ struct Step {
   float lo = 0.0f, hi = 0.0f;
   int32_t fp32 = 0;  // IO steps: boundary side is fp32
   int32_t in_kind = 0;  // direct conv reading the boundary input: 1 fp16, 2 fp32
+  bool cached_out = false;  // ConvBlock: plain output stores (the next step is HBM-bound)
 };
 
 // One input shape's launch list and activation buffers.

@@ -198,3 +198,50 @@ def test_engine_fused_blocks_1080p(builder):
     d = _rel_rms(fused, plain)
     print(spec.name, "1080p fused vs unfused rel RMS %.3g" % d)
     assert d <= (4e-3 if spec.name == "r8f64" else 3e-2), d
+
+
+@pytest.mark.parametrize("builder,want", [
+    (models.r8f64, [False] * 7 + [True]),      # the last block feeds the tail
+    (models.shipped_like, [False] * 7 + [True]),  # the last block feeds the residual conv
+], ids=["r8f64", "shipped_like"])
+def test_plain_stores_only_before_hbm_bound_steps(builder, want):
+    """A fused block stores with plain stores only where the next launch is
+    HBM-bound (the tail, a conv with residual inputs); blocks followed by
+    another block or by a conv without residual inputs keep non-temporal
+    stores. The store policy does not change a value: the output still matches
+    the same model with every conv launched alone."""
+    spec = builder(seed=1)
+    x = models.synthetic_input((1, 1, 40, 72), seed=9)
+    with Engine(0) as e:
+        e.build(spec)
+        e.set_profiling(True)
+        e.profile_read()
+        fused = e.run(x)
+        steps = [nm for nm, _, _ in e.profile_read()]
+    blocks = [nm for nm in steps if nm.startswith("winograd_block")]
+    assert [("+cached_out" in nm) for nm in blocks] == want, steps
+    assert not any("+cached_out" in nm for nm in steps if not nm.startswith("winograd_block"))
+    from oracle.model import run_model
+    want_y = run_model(spec.model, x)
+    floor = _rel_rms(run_model(spec.model, x, round_fp16=False), want_y)
+    assert _rel_rms(fused.astype(np.float32), want_y) <= max(4 * floor, 2e-3)
+
+
+@pytest.mark.parametrize("shape,cached", [((1, 1, 1080, 1920), True), ((1, 1, 2160, 3840), False)],
+                         ids=["1080p", "4k"])
+def test_plain_stores_only_for_outputs_that_fit_the_cache(shape, cached):
+    """The last R8F64 block stores plainly at 1080p (a 266 MB output) but not at
+    4K (1.06 GB), where the last-level cache cannot hold the output for the
+    tail."""
+    spec = models.r8f64(seed=1)
+    x = models.synthetic_input(shape, seed=9)
+    with Engine(0) as e:
+        e.build(spec)
+        e.set_profiling(True)
+        e.profile_read()
+        y = e.run(x)
+        steps = [nm for nm, _, _ in e.profile_read()]
+    blocks = [nm for nm in steps if nm.startswith("winograd_block")]
+    assert len(blocks) == 8, steps
+    assert [("+cached_out" in nm) for nm in blocks] == [False] * 7 + [cached], steps
+    assert np.isfinite(y).all()
