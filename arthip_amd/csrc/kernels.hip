@@ -1963,10 +1963,16 @@ __global__ void __launch_bounds__(256) direct_conv_c1_mfma(DirectArgs a, int n_s
     }
   };
 
-  _Float16 cur[3], nxt[3];
-  load_b(begin, cur);
-  for (int it = begin; it < end; ++it) {
-    if (it + 1 < end) load_b(it + 1, nxt);
+  // Items go in batches of kBatch: the batch's input loads all go out first
+  // (indices clamped to the workgroup's last item, so every load is inside
+  // the input), then the items run in order, each waiting only for its own
+  // loads while later items' loads and earlier items' stores stay in flight.
+  // With one item's loads prefetched per iteration instead, the compiler
+  // packed the prefetched values right after requesting them and so waited
+  // there, and that wait (vmcnt also counts stores) drained the item's stores
+  // as well: one full load latency per item.
+  constexpr int kBatch = 4;
+  auto item = [&](int it, const _Float16 (&cur)[3]) {
     int n, sg, y;
     decode(it, n, sg, y);
     const int x0 = SEG * sg;
@@ -1993,8 +1999,14 @@ __global__ void __launch_bounds__(256) direct_conv_c1_mfma(DirectArgs a, int n_s
       const int g = 64 * st + rl;
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, wl[swz(g)]), rs, wbase + 16 * g, 0, 0);
     }
+  };
+  for (int it = begin; it < end; it += kBatch) {
+    _Float16 v[kBatch][3];
 #pragma unroll
-    for (int e = 0; e < 3; ++e) cur[e] = nxt[e];
+    for (int u = 0; u < kBatch; ++u) load_b(min(it + u, end - 1), v[u]);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (it + u < end) item(it + u, v[u]);
   }
 }
 
