@@ -128,15 +128,7 @@ template <int ACT>
 __device__ __forceinline__ h4 fast4(f4 y, f4 bias4, h4 s0, h4 s1) {
   h4 r = to_h4(y + bias4);
   if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
-  if (ACT == kActSilu) {
-    f4 t;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x = (float)r[e];
-      t[e] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
-    }
-    r = to_h4(t);
-  }
+  if (ACT == kActSilu) r = silu4(r);
   r += s0;
   r += s1;
   return r;

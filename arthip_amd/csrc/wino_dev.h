@@ -135,20 +135,28 @@ __device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16
   v_transform<StripLds<KC>::WPS>(vw, top, bot);
 }
 
+// SiLU of four fp16 values, x / (1 + exp(-x)) in fp32 and one rounding to
+// fp16: exp(-x) as exp2 of x * -log2(e) (what __expf(-x) computes), the
+// reciprocal, and x times it. Both products are FMAs with a zero addend, which
+// take x in fp16 directly (v_fma_mix_f32), so x is never converted on its own;
+// the values equal plain products except that a zero result is +0.
+__device__ __forceinline__ h4 silu4(h4 r) {
+  f4 t;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float x = (float)r[e];
+    const float q = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(x, -1.44269502f, 0.0f)));
+    t[e] = __builtin_fmaf(x, q, 0.0f);
+  }
+  return __builtin_convertvector(t, h4);
+}
+
 // fp16 rounding and activation of 4 channels whose accumulator holds the bias.
 template <int ACT>
 __device__ __forceinline__ h4 strip_act4(f4 y) {
   h4 r = to_h4(y);
   if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
-  if (ACT == kActSilu) {
-    f4 t;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float x = (float)r[e];
-      t[e] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
-    }
-    r = to_h4(t);
-  }
+  if (ACT == kActSilu) r = silu4(r);
   return r;
 }
 
@@ -190,11 +198,9 @@ template <int ACT>
 __device__ __forceinline__ h8 act8(h8 r) {
   if (ACT == kActRelu) r = __builtin_elementwise_max(r, h8{0, 0, 0, 0, 0, 0, 0, 0});
   if (ACT == kActSilu) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = (float)r[e];
-      r[e] = (_Float16)(x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)));
-    }
+    const h4 lo = silu4(__builtin_shufflevector(r, r, 0, 1, 2, 3));
+    const h4 hi = silu4(__builtin_shufflevector(r, r, 4, 5, 6, 7));
+    r = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   }
   return r;
 }
