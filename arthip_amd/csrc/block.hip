@@ -45,7 +45,8 @@ namespace arthip {
 // the workgroup barrier:
 //   conv1 waves: store output row k-5 from staging[(k-5)&1] with its
 //                residuals (k >= 5) and load the residuals of row k-4 (up to
-//                one residual input; with two the conv2 waves do both);
+//                one residual input; with two, only the first row of each
+//                pair, and the conv2 waves store and load the second);
 //                transform t_k into V1'[k&1] (k <= len) and load the input
 //                rows of t_{k+1}; fold t_{k-1} from V1'[(k-1)&1] into ring
 //                slot (k-1)&1 (1 <= k <= len+1)
@@ -57,6 +58,7 @@ namespace arthip {
 // the conv1 waves where it can: with the conv2 waves it made theirs the
 // longer chain by about a third of a phase (timestamps per section), and
 // moved over it took the 1080p one-residual launch from 240 to 226 us.
+// With two residual inputs it is split between the two wave groups.
 struct BlockL {
   static constexpr int C = 64;
   static constexpr int PX = 2 * C;                // bytes per pixel
@@ -190,12 +192,15 @@ winograd_block(BlockArgs a) {
   const int tt = gtid >> 4;
   const int tq = gtid & 15;
 
-  // Store phase: thread handles 16-byte group sg of pixel sx in both rows of
-  // the output row pair that left the conv2 fold last phase. The conv1 waves
-  // run it with up to one residual input; with two, the residual registers
-  // held across the conv1 fold cost more than the store saves the conv2
-  // waves (1080p: 280 us against 260), so the conv2 waves keep it.
-  constexpr bool kConv1Stores = NSKIP < 2;
+  // Store phase: thread handles 16-byte group sg of pixel sx in a row of the
+  // output row pair that left the conv2 fold last phase. With up to one
+  // residual input the conv1 waves store both rows (1080p, one residual:
+  // 240 us with the conv2 waves storing, 226 with conv1; split, 229). With
+  // two, holding both rows' residual registers across the conv1 fold costs
+  // more than it saves (280 against 260 us), so the rows are split: the conv1
+  // waves store row 0 and the conv2 waves row 1, each holding one row's
+  // residuals (259 -> 241 us).
+  constexpr int kConv1Rows = NSKIP < 2 ? 2 : 1;  // rows [0, kConv1Rows) in conv1
   // With act1 ReLU or none, conv1 runs on U1' / 4 and bias1 / 4 and the ring
   // holds t / 4: the power-of-two scale commutes with the activation and with
   // every fp16 and fp32 rounding (outside the subnormal range), so conv2's
@@ -225,7 +230,8 @@ winograd_block(BlockArgs a) {
     const bool ok = live && (r == 0 || 2 * o + 1 < a.H);  // uniform
     return ok ? lane_off + (uint32_t)r * rb32 : kOob;
   };
-  auto load_skips = [&](bool live, int o) {
+  // Rows [ra, rb) of the pair.
+  auto load_skips = [&](bool live, int o, int ra, int rb) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
@@ -234,15 +240,15 @@ winograd_block(BlockArgs a) {
     for (int k = 0; k < NSKIP; ++k) {
       const __amdgpu_buffer_rsrc_t rs = row_rsrc(k == 0 ? a.skip0 : a.skip1, o);
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int r = ra; r < rb; ++r)
         skr[k][r] = __builtin_bit_cast(
             h8, __builtin_amdgcn_raw_buffer_load_b128(rs, st_off(live, o, r), 0, kNonTemporal));
     }
   };
-  auto store_row = [&](bool live, int o, int SB) {
+  auto store_row = [&](bool live, int o, int SB, int ra, int rb) {
     const __amdgpu_buffer_rsrc_t rs = row_rsrc(a.out, o);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = ra; r < rb; ++r) {
       h8 v = act8<ACT2>(*reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C));
       if (NSKIP > 0) v += skr[0][r];
       if (NSKIP > 1) v += skr[1][r];
@@ -318,10 +324,8 @@ winograd_block(BlockArgs a) {
       // Output row k-5 leaves staging (k-5)&1 = P^1 (the conv2 fold of the
       // last phase); its residuals were loaded last phase. Then the residuals
       // of row k-4 (folded by conv2 this phase, stored next phase).
-      if constexpr (kConv1Stores) {
-        store_row(k >= 5, j0 + k - 5, P ^ 1);
-        load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
-      }
+      store_row(k >= 5, j0 + k - 5, P ^ 1, 0, kConv1Rows);
+      load_skips(k >= 4 && k <= len + 3, j0 + k - 4, 0, kConv1Rows);
       // Transform first, fold second: the conv2 wave on the same SIMD folds
       // first, so one wave's VALU transform overlaps the other's MFMA chain
       // (and the next input rows are requested earlier).
@@ -423,7 +427,7 @@ winograd_block(BlockArgs a) {
     h2(&nxt)[16] = P ? A : B;
     // Output row k-5 leaves staging (k-5)&1 = P^1; its residuals were loaded
     // last phase.
-    if constexpr (!kConv1Stores) store_row(k >= 5, j0 + k - 5, P ^ 1);
+    if constexpr (kConv1Rows < 2) store_row(k >= 5, j0 + k - 5, P ^ 1, kConv1Rows, 2);
     const bool fold = k >= 4 && k <= len + 3;
     if (fold) {
       f4 y00, y01, y10, y11;
@@ -436,7 +440,7 @@ winograd_block(BlockArgs a) {
     }
     // Residual inputs of the row just folded (stored next phase); issued after
     // the fold so that they are not live across it.
-    if constexpr (!kConv1Stores) load_skips(fold, j0 + k - 4);
+    if constexpr (kConv1Rows < 2) load_skips(fold, j0 + k - 4, kConv1Rows, 2);
     if (k >= 2 && k <= len + 2) {
       // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is
       // the patch of output row k-3.
