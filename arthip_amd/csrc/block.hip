@@ -201,6 +201,12 @@ winograd_block(BlockArgs a) {
   // waves store row 0 and the conv2 waves row 1, each holding one row's
   // residuals (259 -> 241 us).
   constexpr int kConv1Rows = NSKIP < 2 ? 2 : 1;  // rows [0, kConv1Rows) in conv1
+  // The conv1 waves load the next row's residuals right after the store, or,
+  // in the ReLU / no-activation block with one residual input, after their
+  // fold, so that those registers are not live across it: that block 227.0
+  // -> 224.6 us at 1080p, while the same order took the SiLU block from 265 to
+  // 284-293 us and the two-residual block from 240 to 260 us.
+  constexpr bool kSkipsAfterFold = ACT1 != kActSilu && NSKIP == 1;
   // With act1 ReLU or none, conv1 runs on U1' / 4 and bias1 / 4 and the ring
   // holds t / 4: the power-of-two scale commutes with the activation and with
   // every fp16 and fp32 rounding (outside the subnormal range), so conv2's
@@ -325,7 +331,8 @@ winograd_block(BlockArgs a) {
       // last phase); its residuals were loaded last phase. Then the residuals
       // of row k-4 (folded by conv2 this phase, stored next phase).
       store_row(k >= 5, j0 + k - 5, P ^ 1, 0, kConv1Rows);
-      load_skips(k >= 4 && k <= len + 3, j0 + k - 4, 0, kConv1Rows);
+      if constexpr (!kSkipsAfterFold)
+        load_skips(k >= 4 && k <= len + 3, j0 + k - 4, 0, kConv1Rows);
       // Transform first, fold second: the conv2 wave on the same SIMD folds
       // first, so one wave's VALU transform overlaps the other's MFMA chain
       // (and the next input rows are requested earlier).
@@ -354,6 +361,8 @@ winograd_block(BlockArgs a) {
         *reinterpret_cast<u2*>(sl + rw[2]) = masked(y10, rm1 & cm0);
         *reinterpret_cast<u2*>(sl + rw[3]) = masked(y11, rm1 & cm1);
       }
+      if constexpr (kSkipsAfterFold)
+        load_skips(k >= 4 && k <= len + 3, j0 + k - 4, 0, kConv1Rows);
       lds_sync();
     };
     for (int it = begin; it < end;) {
