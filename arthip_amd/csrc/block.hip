@@ -441,9 +441,6 @@ winograd_block(BlockArgs a) {
     constexpr int P = decltype(par_tag)::value;  // k & 1
     h2(&cur)[16] = P ? B : A;
     h2(&nxt)[16] = P ? A : B;
-    // Output row k-5 leaves staging (k-5)&1 = P^1; its residuals were loaded
-    // last phase.
-    if constexpr (kConv1Rows < 2) store_row(k >= 5, j0 + k - 5, P ^ 1, kConv1Rows, 2);
     // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is the
     // patch of output row k-3.
     if constexpr (kRingEarly)
@@ -458,9 +455,14 @@ winograd_block(BlockArgs a) {
       *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<kActNone>(y10);
       *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<kActNone>(y11);
     }
-    // Residual inputs of the row just folded (stored next phase); issued after
-    // the fold so that they are not live across it.
-    if constexpr (kConv1Rows < 2) load_skips(fold, j0 + k - 4, kConv1Rows, 2);
+    // With two residual inputs: output row k-5 leaves staging (k-5)&1 = P^1
+    // with the residuals loaded last phase (after the fold: 243 -> 235 us
+    // against before it), then the residuals of the row just folded (stored
+    // next phase), issued after the fold so that they are not live across it.
+    if constexpr (kConv1Rows < 2) {
+      store_row(k >= 5, j0 + k - 5, P ^ 1, kConv1Rows, 2);
+      load_skips(fold, j0 + k - 4, kConv1Rows, 2);
+    }
     if (k >= 2 && k <= len + 2) {
       if constexpr (!kRingEarly) ring_load2(nxt, P);
       if (k >= 3) v_transform<WPS, !kQuarterT>(vw + (P ^ 1) * VBUF, cur, nxt);
