@@ -50,11 +50,11 @@ namespace arthip {
 //                transform t_k into V1'[k&1] (k <= len) and load the input
 //                rows of t_{k+1}; fold t_{k-1} from V1'[(k-1)&1] into ring
 //                slot (k-1)&1 (1 <= k <= len+1)
-//   conv2 waves: read t_{k-2} from ring slot k&1 (before the fold with up
-//                to one residual input, after it with two); fold output row
-//                k-4 from V2'[k&1] into staging[k&1] (4 <= k <= len+3);
-//                transform output row k-3 into V2'[(k-3)&1] (3 <= k <= len+2;
-//                at k = 2 only the read)
+//   conv2 waves: read t_{k-2} from ring slot k&1 (2 <= k <= len+2); fold
+//                output row k-4 from V2'[k&1] into staging[k&1]
+//                (4 <= k <= len+3); with two residual inputs store the second
+//                row of output row pair k-5 and load the residuals of row k-4;
+//                transform output row k-3 into V2'[(k-3)&1] (3 <= k <= len+2)
 // Every buffer's writer and readers are a barrier apart. The store sits with
 // the conv1 waves where it can: with the conv2 waves it made theirs the
 // longer chain by about a third of a phase (timestamps per section), and
@@ -208,12 +208,6 @@ winograd_block(BlockArgs a) {
   // -> 224.6 us at 1080p, while the same order took the SiLU block from 265 to
   // 284-293 us and the two-residual block from 240 to 260 us.
   constexpr bool kSkipsAfterFold = ACT1 != kActSilu && NSKIP == 1;
-  // The conv2 waves read t from the ring at the start of the phase, so that
-  // those LDS reads overlap their fold (the registers they land in are live
-  // all phase anyway), except with two residual inputs, where the conv2 waves
-  // also store and load a row: one-residual block 222.0 -> 219.8 us, SiLU
-  // block 260 -> 255 us, two-residual block 239 -> 243 us.
-  constexpr bool kRingEarly = NSKIP < 2;
   // With act1 ReLU or none, conv1 runs on U1' / 4 and bias1 / 4 and the ring
   // holds t / 4: the power-of-two scale commutes with the activation and with
   // every fp16 and fp32 rounding (outside the subnormal range), so conv2's
@@ -442,9 +436,11 @@ winograd_block(BlockArgs a) {
     h2(&cur)[16] = P ? B : A;
     h2(&nxt)[16] = P ? A : B;
     // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is the
-    // patch of output row k-3.
-    if constexpr (kRingEarly)
-      if (k >= 2 && k <= len + 2) ring_load2(nxt, P);
+    // patch of output row k-3. Read at the start of the phase, so that these
+    // LDS reads overlap the fold (the registers they land in are live all phase
+    // anyway): one-residual block 222.0 -> 219.8 us, SiLU block 260 -> 255 us,
+    // two-residual block (its store after the fold) 230.9 -> 228.6 us.
+    if (k >= 2 && k <= len + 2) ring_load2(nxt, P);
     const bool fold = k >= 4 && k <= len + 3;
     if (fold) {
       f4 y00, y01, y10, y11;
@@ -464,7 +460,6 @@ winograd_block(BlockArgs a) {
       load_skips(fold, j0 + k - 4, kConv1Rows, 2);
     }
     if (k >= 2 && k <= len + 2) {
-      if constexpr (!kRingEarly) ring_load2(nxt, P);
       if (k >= 3) v_transform<WPS, !kQuarterT>(vw + (P ^ 1) * VBUF, cur, nxt);
     }
     lds_sync();
