@@ -25,10 +25,11 @@ namespace arthip {
 // column offset -1), one tile row (2 t rows) per step, into a 2-slot LDS ring;
 // t outside the image is stored as zero, which is conv2's padding. Waves 4-7
 // (conv2) hold U2', transform t from the ring (keeping the previous two rows in
-// registers), fold 16 tiles of which the first 15 are the strip's outputs,
-// stage them and store them with the residual inputs added (loaded one step
-// ahead; the block input rows were read by conv1 a few steps before and are
-// usually still cached).
+// registers), fold 16 tiles of which the first 15 are the strip's outputs and
+// stage them. The staged rows go to HBM a step later with the residual inputs
+// added (loaded one step ahead; the block input rows were read by conv1 a few
+// steps before and are usually still cached): stored by the conv1 waves, or
+// with two residual inputs one row of each pair by each group.
 //
 // Both halves are winograd_strip's arithmetic: the same V' transform, fold
 // order and fp16 roundings. conv1's tiles sit at odd offsets (t columns
@@ -44,9 +45,10 @@ namespace arthip {
 // rows 2(j0+i)-1 and 2(j0+i), i = 0 .. len), phase k (k = 0 .. len+4) ends with
 // the workgroup barrier:
 //   conv1 waves: store output row k-5 from staging[(k-5)&1] with its
-//                residuals (k >= 5) and load the residuals of row k-4 (up to
-//                one residual input; with two, only the first row of each
-//                pair, and the conv2 waves store and load the second);
+//                residuals (k >= 5) and load the residuals of row k-4 (after
+//                the fold in the ReLU / no-activation block with one residual
+//                input; with two, only the first row of each pair, and the
+//                conv2 waves store and load the second);
 //                transform t_k into V1'[k&1] (k <= len) and load the input
 //                rows of t_{k+1}; fold t_{k-1} from V1'[(k-1)&1] into ring
 //                slot (k-1)&1 (1 <= k <= len+1)
