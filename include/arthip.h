@@ -358,8 +358,10 @@ int arthip_conv3x3_f16_nhwc(const void* in, const void* packed, const float* bia
  * with two arthip_conv3x3_f16_nhwc calls to fp16 rounding (same error against
  * an exact reference), not bit for bit; it is bit-stable. packed1 / bias1 and packed2 /
  * bias2 come from arthip_conv3x3_pack. act1: 0 none, 1 ReLU, 2 SiLU. skip1
- * only with skip0; out must not alias in or a skip. Returns 1 for other
- * channel counts or a padded image of 2 GiB or more. */
+ * only with skip0; out must not alias in or a skip. The output stores carry
+ * the non-temporal hint (an engine plan uses plain ones when the next launch
+ * reads the output from HBM and it fits the last-level cache). Returns 1 for
+ * other channel counts or a padded image of 2 GiB or more. */
 int arthip_conv3x3_block_f16_nhwc(const void* in, const void* packed1, const float* bias1,
                                   int act1, const void* packed2, const float* bias2,
                                   const void* skip0, const void* skip1, void* out, int N, int H,
