@@ -118,6 +118,17 @@ def test_block_geometry(h, w):
     _check_block(x, ws, bs, skips, 1, f"{h}x{w}")
 
 
+@pytest.mark.parametrize("h,w", EDGES + [(33, 33), (54, 1920)])
+@pytest.mark.parametrize("act1,nskip", [(0, 2), (1, 2), (2, 1), (1, 0)])
+def test_block_geometry_other_epilogues(h, w, act1, nskip):
+    """The strip-width edge cases and two larger frames for the kernel's other
+    store arrangements: with two residual inputs each output row pair's store is
+    split between the two wave groups, with ReLU / no activation and one input
+    the residual loads follow the conv1 fold, with SiLU they precede it."""
+    x, ws, bs, skips = _case(h * 1000 + w + 97 * nskip + act1, 1, h, w, nskip)
+    _check_block(x, ws, bs, skips, act1, f"{h}x{w} act1={act1} nskip={nskip}")
+
+
 @pytest.mark.parametrize("act1", [0, 1, 2])
 @pytest.mark.parametrize("nskip", [0, 1, 2])
 def test_block_epilogues(act1, nskip):
