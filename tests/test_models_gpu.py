@@ -146,19 +146,64 @@ def _band_check(got_full, spec, x, r0, r1, margin, c0=0, c1=None):
     return _compare(got, want), _compare(want, exact)
 
 
-def test_r8f64_full_1080p_band_parity():
-    """Full-size frame on the GPU; the oracle checks a 32-row band in the middle
-    (receptive field of 18 3x3 convs = 18 rows of margin)."""
-    spec = models.r8f64(seed=0)
-    x = models.synthetic_input((1, 1, 1080, 1920), seed=1)
-    with Engine(0) as e:
-        got = e.build(spec).run(x).astype(np.float32)
-        again = e.run(x)
-    np.testing.assert_array_equal(got, again.astype(np.float32))
-    assert got.shape == (1, 1, 2160, 3840) and np.isfinite(got).all()
-    s, floor = _band_check(got, spec, x, 520, 552, 18)
-    print("r8f64 1080p band", s, "floor", floor)
-    assert s["rel_rms"] <= max(FLOOR_RATIO * floor["rel_rms"], 2e-3), (s, floor)
+#: Full-frame oracle outputs, computed once per (workload, mode) and shared by
+#: the tests of both modes (each full 1080p oracle run takes tens of seconds).
+_ORACLE_FULL: dict = {}
+_GPU_FULL: dict = {}
+
+
+def _oracle_full(key, model, x, round_fp16):
+    k = (key, round_fp16)
+    if k not in _ORACLE_FULL:
+        _ORACLE_FULL[k] = run_model(model, x, round_fp16=round_fp16).astype(np.float32)
+    return _ORACLE_FULL[k]
+
+
+def _r8f64_1080p():
+    """R8F64 on one 1920x1080 frame through the engine, twice (bit-stability)."""
+    if not _GPU_FULL.get("r8f64"):
+        spec = models.r8f64(seed=0)
+        x = models.synthetic_input((1, 1, 1080, 1920), seed=1)
+        with Engine(0) as e:
+            got = e.build(spec).run(x)
+            again = e.run(x)
+        _GPU_FULL["r8f64"] = (spec, x, got, again)
+    return _GPU_FULL["r8f64"]
+
+
+#: R8F64 at 1080p, whole frame: largest per-element error against the oracle
+#: (outputs up to ~370 in magnitude). The engine measures 0.81 against the
+#: fp16-storage oracle and 0.68 against fp32 throughout (the two oracle modes
+#: differ by up to 0.46); the bounds sit 1.5x above. A wrong tile, strip edge or
+#: run boundary gives errors of the order of the outputs themselves.
+R8F64_FULL_MAX_ABS = {True: 1.25, False: 1.05}
+
+
+@pytest.mark.parametrize("round_fp16", [True, False], ids=["fp16_storage", "fp32_throughout"])
+def test_r8f64_full_1080p_every_pixel(round_fp16):
+    """Full-size frame on the GPU, every output pixel against the oracle in the
+    given mode: relative RMS within 3x the model's fp16-storage floor (the
+    oracle in one mode against the other, over the whole frame) and a
+    per-element max-abs bound."""
+    spec, x, got, again = _r8f64_1080p()
+    assert got.shape == (1, 1, 2160, 3840)
+    np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16))
+    got = got.astype(np.float32)
+    assert np.isfinite(got).all()
+    want = _oracle_full("r8f64", spec.model, x, round_fp16)
+    floor = _compare(_oracle_full("r8f64", spec.model, x, True),
+                     _oracle_full("r8f64", spec.model, x, False))
+    s = _compare(got, want)
+    err = np.abs(got.astype(np.float64) - want)
+    # Error per 60x64-pixel output block (one 30-pixel strip x 16 tile rows of
+    # the input): a defect confined to one workgroup's run shows up here.
+    blocks = err[0, 0, :2160 // 64 * 64, :3840 // 60 * 60].reshape(2160 // 64, 64, 3840 // 60, 60)
+    block_rms = np.sqrt((blocks ** 2).mean(axis=(1, 3)))
+    print("r8f64 1080p full frame", "fp16 storage" if round_fp16 else "fp32 throughout", s,
+          "floor", floor, "ratio %.3f" % (s["rel_rms"] / floor["rel_rms"]),
+          "block RMS max %.4f median %.4f" % (block_rms.max(), np.median(block_rms)))
+    assert s["rel_rms"] <= FLOOR_RATIO * floor["rel_rms"], (s, floor)
+    assert s["max_abs"] <= R8F64_FULL_MAX_ABS[round_fp16], s
 
 
 def test_r16f96_full_1080p_window_parity():
@@ -226,43 +271,79 @@ def _shipped_model():
 SHIPPED_MAX_ABS = 1.34e-3
 
 
-def test_shipped_model_on_real_image_meets_gate():
-    """The reference's shipped luma model on its own 256x256 test image: bounded
-    [0,1] output, so the literal gate applies, and the reference's 1e-3 class."""
-    x = _gray8("test_256.png")
-    model = _shipped_model()
-    with Engine(0) as e:
-        got = e.build(model).run(x).astype(np.float32)
-    assert got.shape == (1, 1, 512, 512) and np.isfinite(got).all()
-    _literal_gate(got, model, x, "shipped luma 256x256", max_abs=SHIPPED_MAX_ABS)
+def _code_mismatch(got, want):
+    """Fraction of output samples whose 8-bit codes differ, the reference's
+    accuracy tool's second gate (tests/tools/multires.py:62-73,202-208):
+    round(v * 255) half to even, clipped to [0, 255]."""
+    def code(v):
+        return np.clip(np.round(np.asarray(v, np.float32) * 255), 0, 255).astype(np.uint8)
+    return float((code(got) != code(want)).mean())
 
 
-def test_shipped_model_full_1920_real_image():
-    """The product's real workload: the shipped luma model on the reference's
-    1920x1080 test photo at full size (the reference's accuracy gate,
-    NOTES.md:78-79). Finite, bit-stable across runs, and four windows (the two
-    corners, the middle, and a right-edge band) against the oracle in both modes,
-    with a 28-pixel margin (27 convs)."""
-    x = _gray8("test_1920.png")
-    assert x.shape == (1, 1, 1080, 1920)
+#: Fraction of 8-bit codes allowed to differ (multires.py:67-73: the reference
+#: measures 1.0-2.0 % against ONNX Runtime CPU).
+SHIPPED_MISMATCH = 0.025
+
+
+def _shipped_gates(got, model, x, key, label):
+    """Literal gates of the shipped model against the oracle in both modes:
+    max-abs <= SHIPPED_MAX_ABS, PSNR >= 50 dB and <= 2.5 % 8-bit code
+    mismatches, every pixel."""
+    for mode in (True, False):
+        want = _oracle_full(key, model, x, mode)
+        s = _compare(got, want)
+        s["mismatch"] = _code_mismatch(got, want)
+        print(label, "fp16 storage" if mode else "fp32 throughout", s)
+        assert s["max_abs"] <= SHIPPED_MAX_ABS and s["psnr"] >= 50.0, (mode, s)
+        assert s["mismatch"] <= SHIPPED_MISMATCH, (mode, s)
+
+
+@pytest.mark.parametrize("image", ["test_256.png", "test_512.png", "test_1024.png"])
+def test_shipped_model_on_real_images(image):
+    """The reference's shipped luma model on its own test images at the sizes its
+    accuracy sweep feeds (multires.py:73: 256, 512, 1024), whole frames: bounded
+    [0,1] output, so the literal gates apply, and the reference's 1e-3 class."""
+    x = _gray8(image)
     model = _shipped_model()
     with Engine(0) as e:
         got = e.build(model).run(x)
         again = e.run(x)
-    assert got.shape == (1, 1, 2160, 3840) and np.isfinite(got).all()
+    n = x.shape[2]
+    assert got.shape == (1, 1, 2 * n, 2 * n) and np.isfinite(got.astype(np.float32)).all()
+    np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16))
+    _shipped_gates(got.astype(np.float32), model, x, image, "shipped luma %s" % image)
+
+
+def _shipped_1920():
+    if not _GPU_FULL.get("shipped"):
+        x = _gray8("test_1920.png")
+        assert x.shape == (1, 1, 1080, 1920)
+        model = _shipped_model()
+        with Engine(0) as e:
+            got = e.build(model).run(x)
+            again = e.run(x)
+        _GPU_FULL["shipped"] = (model, x, got, again)
+    return _GPU_FULL["shipped"]
+
+
+@pytest.mark.parametrize("round_fp16", [True, False], ids=["fp16_storage", "fp32_throughout"])
+def test_shipped_model_full_1920_real_image(round_fp16):
+    """The product's real workload: the shipped luma model on the reference's
+    1920x1080 test photo, the whole frame against the oracle in the given mode
+    (the reference's accuracy gate, NOTES.md:78-79, and its 8-bit code
+    mismatch gate); bit-stable across runs."""
+    model, x, got, again = _shipped_1920()
+    assert got.shape == (1, 1, 2160, 3840)
     np.testing.assert_array_equal(got.view(np.uint16), again.view(np.uint16))
     got = got.astype(np.float32)
-    worst = {True: 0.0, False: 0.0}
-    for r0, r1, c0, c1 in ((0, 32, 0, 128), (524, 556, 896, 1024), (1048, 1080, 1792, 1920),
-                           (300, 332, 1792, 1920)):
-        part = got[:, :, 2 * r0:2 * r1, 2 * c0:2 * c1]
-        for mode in (True, False):
-            want = _window_oracle(model, x, r0, r1, c0, c1, 28, 2, round_fp16=mode)
-            s = _compare(part, want)
-            worst[mode] = max(worst[mode], s["max_abs"])
-            assert s["max_abs"] <= SHIPPED_MAX_ABS and s["psnr"] >= 50.0, ((r0, c0), mode, s)
-    print("shipped luma 1920x1080 max-abs vs oracle: fp16 storage %.5f, fp32 throughout %.5f "
-          "(reference vs ONNX Runtime CPU: 0.00134)" % (worst[True], worst[False]))
+    assert np.isfinite(got).all()
+    want = _oracle_full("test_1920.png", model, x, round_fp16)
+    s = _compare(got, want)
+    s["mismatch"] = _code_mismatch(got, want)
+    print("shipped luma 1920x1080 full frame", "fp16 storage" if round_fp16 else "fp32 throughout",
+          s, "(reference vs ONNX Runtime CPU: max-abs 0.00134)")
+    assert s["max_abs"] <= SHIPPED_MAX_ABS and s["psnr"] >= 50.0, s
+    assert s["mismatch"] <= SHIPPED_MISMATCH, s
 
 
 def test_r8f64_8k_frame_past_2gib_activations():
