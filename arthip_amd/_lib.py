@@ -82,6 +82,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         c_char, c_int, c_char, c_int)
     sig("arthip_engine_set_debug", c_int, eng, c_int, c_char)
     sig("arthip_engine_get_debug", c_int, eng, i32p)
+    sig("arthip_engine_set_log", c_int, eng, c_char, c_char, c_int)
 
     sig("engine_device_count", c_int, i32p)
     sig("engine_probe", c_int, c_char, c_int, c_int, c_int, c_int, c_int, c_char, c_int,
@@ -133,7 +134,7 @@ EXPORTED_SYMBOLS = (
     "arthip_engine_run", "arthip_engine_run_device", "arthip_engine_run_device_noalloc",
     "arthip_engine_describe",
     "arthip_engine_set_profiling", "arthip_engine_profile_read", "arthip_engine_set_debug",
-    "arthip_engine_get_debug",
+    "arthip_engine_get_debug", "arthip_engine_set_log",
     "engine_device_count", "engine_probe", "engine_run", "engine_alloc_failure_then_run",
     "arthip_ep_get_capability", "arthip_ep_run_boundary", "arthip_ep_node_keys",
     "arthip_engine_build_subgraph",

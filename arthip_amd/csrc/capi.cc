@@ -16,6 +16,16 @@
 #include "launch.h"
 #include "pack.h"
 
+static_assert(ARTHIP_DEBUG_POISON == arthip::kDebugPoison &&
+                  ARTHIP_DEBUG_SYNC_EACH == arthip::kDebugSyncEach &&
+                  ARTHIP_DEBUG_DUMP == arthip::kDebugDump &&
+                  ARTHIP_DEBUG_UNFUSED == arthip::kDebugUnfused &&
+                  ARTHIP_DEBUG_TRACE == arthip::kDebugTrace &&
+                  ARTHIP_DEBUG_HOST_PROFILE == arthip::kDebugHostProfile &&
+                  ARTHIP_DEBUG_DUMPOPS == arthip::kDebugDumpOps &&
+                  ARTHIP_DEBUG_PLAN == arthip::kDebugPlan,
+              "debug flag values of the C ABI and the engine differ");
+
 struct arthip_engine {
   std::unique_ptr<arthip::Engine> eng;
 };
@@ -219,11 +229,21 @@ int arthip_engine_set_debug(arthip_engine* eng, int flags, const char* dump_dir)
   return guard(ARTHIP_ERR_BUILD, nullptr, 0, "", [&]() -> int {
     if (eng == nullptr) return fail("null engine", ARTHIP_ERR_BUILD);
     if ((flags & ~(ARTHIP_DEBUG_POISON | ARTHIP_DEBUG_SYNC_EACH | ARTHIP_DEBUG_DUMP |
-                   ARTHIP_DEBUG_UNFUSED)) != 0)
+                   ARTHIP_DEBUG_UNFUSED | ARTHIP_DEBUG_TRACE | ARTHIP_DEBUG_HOST_PROFILE |
+                   ARTHIP_DEBUG_DUMPOPS | ARTHIP_DEBUG_PLAN)) != 0)
       return fail("unknown debug flag", ARTHIP_ERR_BUILD);
     if ((flags & ARTHIP_DEBUG_DUMP) && (dump_dir == nullptr || *dump_dir == '\0'))
       return fail("dump requested without a directory", ARTHIP_ERR_BUILD);
     eng->eng->SetDebug(flags, dump_dir ? dump_dir : "");
+    return ARTHIP_OK;
+  });
+}
+
+int arthip_engine_set_log(arthip_engine* eng, const char* path, char* err, int errlen) {
+  return guard(ARTHIP_ERR_BUILD, err, errlen, "", [&]() -> int {
+    if (eng == nullptr) return report("null engine", ARTHIP_ERR_BUILD, err, errlen);
+    std::string e;
+    if (!eng->eng->SetLog(path ? path : "", e)) return report(e, ARTHIP_ERR_BUILD, err, errlen);
     return ARTHIP_OK;
   });
 }

@@ -1,5 +1,6 @@
 #include "clip.h"
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -224,6 +225,8 @@ std::unique_ptr<ClipModel> ClipModel::Create(const ClipModelArgs& args, int num_
   {
     const char* e = std::getenv("VSHIP_PROFILE");
     d->profile_ = e != nullptr && e[0] == '1';
+    const char* t = std::getenv("VSHIP_TRACE");
+    d->trace_ = t != nullptr && t[0] == '1';
   }
   int num_streams = args.has_num_streams ? sat(args.num_streams) : 0;
   if (num_streams < 1) num_streams = 1;
@@ -357,7 +360,22 @@ bool ClipModel::GetFrame(const VideoFormat& fmt, const int* plane_w, const int* 
   std::unique_lock<std::mutex> lock;
   Io* io = nullptr;
   Slot& s = Acquire(lock, io);
-  return RunSlot(s, *io, fmt, in_c, in_w, in_h, src, src_stride, dst, dst_stride, error);
+  if (!trace_) return RunSlot(s, *io, fmt, in_c, in_w, in_h, src, src_stride, dst, dst_stride, error);
+  int ei = 0;
+  for (size_t q = 0; q < slots_.size(); ++q)
+    if (slots_[q].get() == &s) ei = static_cast<int>(q);
+  const unsigned long long n = frames_.fetch_add(1);
+  auto now = [] {
+    return (long long)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+  };
+  std::fprintf(stderr, "[trace] enter eng=%d n=%llu t=%lld\n", ei, n, now());
+  std::fflush(stderr);
+  const bool ok = RunSlot(s, *io, fmt, in_c, in_w, in_h, src, src_stride, dst, dst_stride, error);
+  std::fprintf(stderr, "[trace] leave eng=%d n=%llu t=%lld%s\n", ei, n, now(), ok ? "" : " failed");
+  std::fflush(stderr);
+  return ok;
 }
 
 bool ClipModel::RunSlot(Slot& s, Io& io, const VideoFormat& fmt, int in_c, int w, int h,

@@ -110,6 +110,11 @@ class ClipModel {
   // conversion + download span on stderr for the first three frames of each
   // engine and every 128th (hip_engine.cc:1409-1604).
   bool profile_ = false;
+  // VSHIP_TRACE=1 at creation: "[trace] enter" / "[trace] leave" lines on
+  // stderr around each frame's run, with the engine of the pool, the frame's
+  // call number and a steady-clock timestamp in ns (vs_hip.cpp:239-246).
+  bool trace_ = false;
+  std::atomic<unsigned long long> frames_{0};
   int device_ = 0;
   bool fp16_ = true;
   bool in_fp32_ = false, out_fp32_ = false;

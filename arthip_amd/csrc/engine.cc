@@ -1,6 +1,8 @@
 #include "engine.h"
 
 #include <algorithm>
+#include <chrono>
+#include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -39,6 +41,10 @@ Engine::Engine(int device_id) : device_(device_id) {
       dump_dir_ = d;
     }
   }
+  if (on("VSHIP_TRACE")) debug_ |= kDebugTrace;
+  if (on("HIP_PROFILE")) debug_ |= kDebugHostProfile;
+  if (std::getenv("HIP_DUMPOPS") != nullptr) debug_ |= kDebugDumpOps;  // set, any value
+  if (on("VSHIP_DEBUG")) debug_ |= kDebugPlan;
 }
 
 Engine::~Engine() {
@@ -53,11 +59,102 @@ Engine::~Engine() {
     hipStreamDestroy(stream_);
   }
   if (run_done_) hipEventDestroy(run_done_);
+  if (log_) std::fclose(log_);
+}
+
+bool Engine::SetLog(const std::string& path, std::string& error) {
+  std::lock_guard<std::mutex> lock(mu_);
+  FILE* f = nullptr;
+  if (!path.empty()) {
+    f = std::fopen(path.c_str(), "a");
+    if (f == nullptr) {
+      error = "cannot open log file '" + path + "'";
+      return false;
+    }
+  }
+  if (log_) std::fclose(log_);
+  log_ = f;
+  return true;
+}
+
+void Engine::Log(const char* fmt, ...) {
+  FILE* f = log_ ? log_ : stderr;
+  va_list ap;
+  va_start(ap, fmt);
+  std::vfprintf(f, fmt, ap);
+  va_end(ap);
+  std::fflush(f);
+}
+
+// Trace and host-profile lines of one Run / RunDevice call (VSHIP_TRACE,
+// hip_engine.cc:1280-1298,1421-1425,1619; HIP_PROFILE, hip_graph.cc:1213-1447).
+// The destructor reports a call that returned without Done as failed, with
+// the error text it left.
+struct Engine::RunLog {
+  using Clock = std::chrono::steady_clock;
+  Engine& e;
+  const std::string& error;
+  const bool trace, prof, host;
+  uint64_t no = 0;
+  bool done = false;
+  Clock::time_point t0 = Clock::now(), t_built, t_in, t_launched, t_back;
+
+  RunLog(Engine& eng, const char* what, const void* in, bool host_io, const std::string& err)
+      : e(eng), error(err), trace((eng.debug_ & kDebugTrace) != 0),
+        prof((eng.debug_ & kDebugHostProfile) != 0), host(host_io) {
+    if (trace) {
+      no = ++e.run_no_;
+      e.Log("[run] enter #%llu %s in=%p\n", (unsigned long long)no, what, in);
+    }
+  }
+  void Built() {
+    t_built = Clock::now();
+    if (trace) e.Log("[run] built #%llu\n", (unsigned long long)no);
+  }
+  void Uploaded() { t_in = Clock::now(); }
+  void Launched() { t_launched = Clock::now(); }
+  void Back() { t_back = Clock::now(); }
+  static double ms(Clock::time_point a, Clock::time_point b) {
+    return std::chrono::duration<double, std::milli>(b - a).count();
+  }
+  bool Done(const void* out) {
+    done = true;
+    const Clock::time_point t_end = Clock::now();
+    if (prof) {
+      if (host) {
+        e.Log("[hipprof] build=%.3fms memin=%.3fms launch=%.3fms readback+wait=%.3fms\n",
+              ms(t0, t_built), ms(t_built, t_in), ms(t_in, t_launched), ms(t_launched, t_back));
+        e.Log("[hipprof] memout=%.3fms total=%.3fms\n", ms(t_back, t_end), ms(t0, t_end));
+      } else {
+        e.Log("[hipprof] build=%.3fms launch=%.3fms total=%.3fms (device-resident, not waited "
+              "for)\n", ms(t0, t_built), ms(t_built, t_launched), ms(t0, t_end));
+      }
+    }
+    if (trace) e.Log("[run] done #%llu out=%p\n", (unsigned long long)no, out);
+    return true;
+  }
+  ~RunLog() {
+    if (trace && !done)
+      e.Log("[run] fail #%llu: %s\n", (unsigned long long)no, error.c_str());
+  }
+};
+
+std::string Engine::BufLabel(const Plan& p, int idx, const void* in_dev,
+                             const void* out_dev) const {
+  char buf[160];
+  if (idx == kBoundaryIn)
+    std::snprintf(buf, sizeof buf, "input(%p,%.2fMB)", in_dev, p.in_bytes / 1048576.0);
+  else if (idx == kBoundaryOut)
+    std::snprintf(buf, sizeof buf, "output(%p,%.2fMB)", out_dev, p.out_bytes / 1048576.0);
+  else
+    std::snprintf(buf, sizeof buf, "%d(%p,%.2fMB)", idx, p.bufs[idx].ptr,
+                  p.bufs[idx].bytes / 1048576.0);
+  return buf;
 }
 
 void Engine::SetDebug(int flags, const std::string& dump_dir) {
   std::lock_guard<std::mutex> lock(mu_);
-  flags &= kDebugPoison | kDebugSyncEach | kDebugDump | kDebugUnfused;
+  flags &= kDebugAll;
   if ((flags ^ debug_) & kDebugUnfused) {  // the plans depend on it
     FreePlan();
     ClearPlan(scratch_plan_);
@@ -81,6 +178,33 @@ bool Engine::WaitPrevious(hipStream_t s, std::string& error) {
     error = HipErr("hipStreamWaitEvent on the previous run", e);
     return false;
   }
+  return true;
+}
+
+// For a run captured into a HIP graph: its nodes cannot wait on an event
+// recorded outside the capture, so the previous run must already be over.
+bool Engine::PreviousDone(std::string& error) {
+  if (last_stream_ == nullptr) return true;
+  const hipError_t e = hipEventQuery(run_done_);
+  if (e == hipSuccess) {
+    last_stream_ = nullptr;
+    return true;
+  }
+  error = e == hipErrorNotReady
+              ? "the previous run on this handle is still executing; a run captured into a HIP "
+                "graph cannot wait for it (synchronize before capturing)"
+              : HipErr("hipEventQuery of the previous run", e);
+  return false;
+}
+
+static bool StreamCapturing(hipStream_t s, bool& capturing, std::string& error) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(s, &cs);
+  if (e != hipSuccess) {
+    error = HipErr("hipStreamIsCapturing", e);
+    return false;
+  }
+  capturing = cs != hipStreamCaptureStatusNone;
   return true;
 }
 
@@ -125,12 +249,11 @@ bool Engine::Init(std::string& error) {
     return false;
   }
   // Set-up of the no-allocation entry point's scratch on this device (its
-  // address is resolved once per device, here with the device current), so
-  // that entry point's own calls load and resolve nothing. A failure is
-  // reported by that entry point.
-  void* scratch = nullptr;
+  // address resolved and its ordering event created once per device, here
+  // with the device current), so that entry point's own calls create
+  // nothing. A failure is reported by that entry point.
   std::string ignored;
-  (void)scratch_address(device_, &scratch, ignored);
+  (void)scratch_setup(device_, ignored);
   return true;
 }
 
@@ -653,6 +776,17 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
   }
   std::copy(in, in + 4, p.in);
   p.planned = true;
+  // VSHIP_DEBUG (hip_engine.cc:1167-1184): the new plan's launches.
+  if (debug_ & kDebugPlan) {
+    Log("[vship] %s for [%lld,%lld,%lld,%lld]: %zu launches, %zu activation buffers, %zu "
+        "bytes\n", p.scratch ? "scratch plan" : "plan", (long long)in[0], (long long)in[1],
+        (long long)in[2], (long long)in[3], p.steps.size(), p.bufs.size(), p.act_bytes);
+    for (size_t i = 0; i < p.steps.size(); ++i) {
+      const Step& st = p.steps[i];
+      Log("[vship] step%-2zu %s in=%d in2=%d skip=%d,%d out=%d\n", i, StepName(st).c_str(),
+          st.in, st.in2, st.skip[0], st.skip[1], st.out);
+    }
+  }
   return true;
 }
 
@@ -670,18 +804,32 @@ bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream
     if (idx < 0) return 0;
     return p.bufs[idx].bytes;
   };
+  // A run on a capturing stream becomes graph nodes that execute at each
+  // replay. It cannot wait on the previous run's event (recorded outside the
+  // capture), so that run must be over; it records no end event (the caller
+  // orders the replays); and it neither synchronizes (VSHIP_SYNC_EACH is
+  // refused), nor times its launches, nor dumps.
+  bool capturing = false;
+  if (!StreamCapturing(s, capturing, error)) return false;
+  RelaxedCaptureMode relax(capturing);
+  if (capturing && (debug_ & kDebugSyncEach)) {
+    error = "VSHIP_SYNC_EACH synchronizes the stream after every launch, which a stream under "
+            "HIP graph capture does not allow";
+    return false;
+  }
   // Profiling events and dumps create events and host buffers: runs on a
   // scratch plan do neither.
-  const bool profiling = profiling_ && !p.scratch;
+  const bool profiling = profiling_ && !p.scratch && !capturing;
   if (profiling && prof_acc_.size() != p.steps.size()) {
     prof_acc_.assign(p.steps.size(), StepProfile{});
     for (size_t i = 0; i < p.steps.size(); ++i) prof_acc_[i].name = StepName(p.steps[i]);
   }
-  if (!WaitPrevious(s, error)) return false;
+  if (capturing ? !PreviousDone(error) : !WaitPrevious(s, error)) return false;
   // From here on the run's work is on s: later runs order after it even when
   // this one fails part way.
-  last_stream_ = s;
+  if (!capturing) last_stream_ = s;
   auto finish = [&](bool ok) -> bool {
+    if (capturing) return ok;
     const hipError_t r = hipEventRecord(run_done_, s);
     if (r != hipSuccess && ok) {
       error = HipErr("hipEventRecord at the end of a run", r);
@@ -718,8 +866,8 @@ bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream
   }
   // VSHIP_DUMP: each launch's inputs and output as raw files, for the first
   // two runs of the engine. Activations are padded NHWC fp16 buffers.
-  const bool dump =
-      !p.scratch && (debug_ & kDebugDump) != 0 && !dump_dir_.empty() && dump_runs_ < 2;
+  const bool dump = !p.scratch && !capturing && (debug_ & kDebugDump) != 0 &&
+                    !dump_dir_.empty() && dump_runs_ < 2;
   const uint64_t dump_run = dump ? ++dump_runs_ : 0;
 
   for (size_t i = 0; i < p.steps.size(); ++i) {
@@ -824,6 +972,15 @@ bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream
       error = "HIP kernel launch for step " + std::to_string(i) + " failed: " +
               hipGetErrorString(e);
       return finish(false);
+    }
+    if (debug_ & kDebugTrace)
+      Log("[run] #%llu op%zu %s\n", (unsigned long long)run_no_, i, StepName(st).c_str());
+    if (debug_ & kDebugDumpOps) {
+      std::string line = "[dump] op " + std::to_string(i) + " " + StepName(st) + " in=";
+      for (int idx : {st.in, st.in2, st.skip[0], st.skip[1]})
+        if (idx != kNoBuffer) line += BufLabel(p, idx, in_dev, out_dev) + " ";
+      line += "out=" + BufLabel(p, st.out, in_dev, out_dev);
+      Log("%s\n", line.c_str());
     }
     if (profiling) {
       if (hipEventRecord(ev.stop, s) != hipSuccess) {
@@ -948,9 +1105,11 @@ bool Engine::ProfileRead(std::vector<StepProfile>& out, std::string& error) {
 bool Engine::Run(const void* in_host, const int64_t in[4], void* out_host, size_t out_cap,
                  std::string& error) {
   std::lock_guard<std::mutex> lock(mu_);
+  RunLog rl(*this, "run", in_host, true, error);
   (void)hipGetLastError();  // a stale error from an earlier failed call is not this run's
   if (!Init(error)) return false;
   if (!EnsurePlan(plan_, in, error)) return false;
+  rl.Built();
   const size_t in_bytes = plan_.in_bytes, out_bytes = plan_.out_bytes;
   if (in_host == nullptr || out_host == nullptr) {
     error = "null host buffer";
@@ -978,7 +1137,9 @@ bool Engine::Run(const void* in_host, const int64_t in[4], void* out_host, size_
     error = HipErr("HIP input upload", e);
     return false;
   }
+  rl.Uploaded();
   if (!Enqueue(plan_, in_stage_dev_, out_stage_dev_, stream_, error)) return false;
+  rl.Launched();
   if ((e = hipMemcpyAsync(out_pinned_, out_stage_dev_, out_bytes, hipMemcpyDeviceToHost,
                           stream_)) != hipSuccess) {
     error = HipErr("HIP output download", e);
@@ -988,26 +1149,32 @@ bool Engine::Run(const void* in_host, const int64_t in[4], void* out_host, size_
     error = HipErr("HIP stream synchronize", e);
     return false;
   }
+  rl.Back();
   std::memcpy(out_host, out_pinned_, out_bytes);
-  return true;
+  return rl.Done(out_host);
 }
 
 bool Engine::RunDevice(const void* in_dev, const int64_t in[4], void* out_dev,
                        hipStream_t stream, std::string& error) {
   std::lock_guard<std::mutex> lock(mu_);
+  RunLog rl(*this, "run_device", in_dev, false, error);
   (void)hipGetLastError();
   if (!Init(error)) return false;
   if (!EnsurePlan(plan_, in, error)) return false;
+  rl.Built();
   if (in_dev == nullptr || out_dev == nullptr) {
     error = "null device buffer";
     return false;
   }
-  return Enqueue(plan_, in_dev, out_dev, stream ? stream : stream_, error);
+  if (!Enqueue(plan_, in_dev, out_dev, stream ? stream : stream_, error)) return false;
+  rl.Launched();
+  return rl.Done(out_dev);
 }
 
 bool Engine::RunDeviceScratch(const void* in_dev, const int64_t in[4], void* out_dev,
                               hipStream_t stream, std::string& error) {
   std::lock_guard<std::mutex> lock(mu_);
+  RunLog rl(*this, "run_device_noalloc", in_dev, false, error);
   (void)hipGetLastError();
   if (stream_ == nullptr || run_done_ == nullptr || !weights_ready_) {
     error = "the engine is not set up on its device yet: one run (arthip_engine_run or "
@@ -1016,15 +1183,31 @@ bool Engine::RunDeviceScratch(const void* in_dev, const int64_t in[4], void* out
     return false;
   }
   if (!SetDevice(error)) return false;
-  void* scratch = nullptr;
-  if (!scratch_address(device_, &scratch, error)) return false;
-  scratch_plan_.scratch = true;
-  if (!EnsurePlan(scratch_plan_, in, error, scratch, kNoAllocScratchBytes)) return false;
   if (in_dev == nullptr || out_dev == nullptr) {
     error = "null device buffer";
     return false;
   }
-  return Enqueue(scratch_plan_, in_dev, out_dev, stream ? stream : stream_, error);
+  const hipStream_t s = stream ? stream : stream_;
+  bool capturing = false;
+  if (!StreamCapturing(s, capturing, error)) return false;
+  RelaxedCaptureMode relax(capturing);
+  // Every handle on this device shares its scratch: the lease orders this
+  // call after the last one that used it (and holds off the next) until End.
+  ScratchUse use;
+  void* scratch = nullptr;
+  if (!use.Begin(device_, s, capturing, &scratch, error)) return false;
+  scratch_plan_.scratch = true;
+  if (!EnsurePlan(scratch_plan_, in, error, scratch, kNoAllocScratchBytes)) return false;
+  rl.Built();
+  const bool ok = Enqueue(scratch_plan_, in_dev, out_dev, s, error);
+  std::string end_error;
+  if (!use.End(end_error) && ok) {
+    error = end_error;
+    return false;
+  }
+  if (!ok) return false;
+  rl.Launched();
+  return rl.Done(out_dev);
 }
 
 std::string Engine::Describe() const {

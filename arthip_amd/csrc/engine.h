@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdio>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -28,15 +29,24 @@ struct DevBuf {
   Shape geo{};  // activation buffers: the tensor geometry (padded NHWC around it)
 };
 
-// Diagnostics, the reference's environment switches (hip_engine.cc:1310-1349,
-// hip_graph.cc:1231-1248,1356-1365). An engine starts from VSHIP_POISON=1,
-// VSHIP_SYNC_EACH=1 and VSHIP_DUMP=<dir>; SetDebug overrides them.
+// Diagnostics, the reference's environment switches (hip_engine.cc:1167-1184,
+// 1280-1289,1310-1349; hip_graph.cc:131-132,1213-1447,1231-1248,1356-1373). An
+// engine starts from VSHIP_POISON=1, VSHIP_SYNC_EACH=1, VSHIP_DUMP=<dir>,
+// VSHIP_TRACE=1, HIP_PROFILE=1, HIP_DUMPOPS (set) and VSHIP_DEBUG=1; SetDebug
+// overrides them. The last four write lines to the engine's log (stderr
+// unless SetLog names a file).
 enum DebugFlag : int {
-  kDebugPoison = 1,    // before each run, fill every activation interior with fp16 NaN
-  kDebugSyncEach = 2,  // synchronize the launch stream after every launch
-  kDebugDump = 4,      // write each launch's inputs and output (first two runs)
-  kDebugUnfused = 8,   // run every conv as its own launch (no residual-block fusion)
+  kDebugPoison = 1,       // before each run, fill every activation interior with fp16 NaN
+  kDebugSyncEach = 2,     // synchronize the launch stream after every launch
+  kDebugDump = 4,         // write each launch's inputs and output (first two runs)
+  kDebugUnfused = 8,      // run every conv as its own launch (no residual-block fusion)
+  kDebugTrace = 16,       // "[run]" lines: enter, plan ready, each launch, done / fail
+  kDebugHostProfile = 32, // "[hipprof]" host time spans of each run
+  kDebugDumpOps = 64,     // "[dump]" line per launch: its buffers, addresses and sizes
+  kDebugPlan = 128,       // "[vship]" lines describing each new plan's launches
 };
+constexpr int kDebugAll = kDebugPoison | kDebugSyncEach | kDebugDump | kDebugUnfused |
+                          kDebugTrace | kDebugHostProfile | kDebugDumpOps | kDebugPlan;
 
 enum class StepKind {
   InputConvert,
@@ -135,6 +145,9 @@ class Engine {
   // Diagnostics (DebugFlag bits); dump_dir is used with kDebugDump.
   void SetDebug(int flags, const std::string& dump_dir);
   int DebugFlags() const;
+  // Where the trace, host-profile, op-dump and plan lines go: appended to the
+  // file at `path`, or stderr for an empty path.
+  bool SetLog(const std::string& path, std::string& error);
 
   std::string Describe() const;
 
@@ -174,11 +187,18 @@ class Engine {
   hipEvent_t run_done_ = nullptr;
   hipStream_t last_stream_ = nullptr;
   bool WaitPrevious(hipStream_t s, std::string& error);
+  bool PreviousDone(std::string& error);
   bool DrainPrevious();
 
   int debug_ = 0;
   std::string dump_dir_;
   uint64_t dump_runs_ = 0;
+  FILE* log_ = nullptr;  // null: stderr
+  uint64_t run_no_ = 0;  // runs seen by the trace (kDebugTrace)
+  void Log(const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+  std::string BufLabel(const Plan& p, int idx, const void* in_dev, const void* out_dev) const;
+  // kDebugTrace / kDebugHostProfile bookkeeping of one Run / RunDevice call.
+  struct RunLog;
   bool Dump(const std::string& path, const void* dev, size_t bytes, hipStream_t s);
   Graph graph_;
   bool built_ = false;

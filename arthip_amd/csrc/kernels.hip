@@ -33,6 +33,7 @@
 // output fold absorbs the sign, so U' is not negated.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 
 #include "conv_args.h"
@@ -2363,18 +2364,22 @@ __global__ void __launch_bounds__(256) plane_convert(PlaneArgs a) {
 // ---------------------------------------------------------------------------
 
 namespace {
-int g_cu_count = 0;
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];  // 0: not queried yet
 }  // namespace
 
 int cu_count() {
-  if (g_cu_count == 0) {
-    int dev = 0;
-    hipGetDevice(&dev);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+  int n = g_cu_count[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    // Threads that race here all store the same value.
     hipDeviceProp_t p{};
-    if (hipGetDeviceProperties(&p, dev) == hipSuccess) g_cu_count = p.multiProcessorCount;
-    if (g_cu_count <= 0) g_cu_count = 256;
+    if (hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+    if (n <= 0) n = 256;
+    g_cu_count[dev].store(n, std::memory_order_relaxed);
   }
-  return g_cu_count;
+  return n;
 }
 
 FastDiv make_fastdiv(uint32_t d) {

@@ -12,7 +12,8 @@
 
 namespace arthip {
 
-// Compute units of the current device (queried once; 256 when unknown).
+// Compute units of the current device (queried once per device, thread-safe;
+// 256 when unknown).
 int cu_count();
 // Multiply-shift constants for dividing uniform values < 2^31 by d on the GPU.
 FastDiv make_fastdiv(uint32_t d);
@@ -43,11 +44,57 @@ hipError_t launch_poison(void* buf, int32_t N, int32_t H, int32_t W, int32_t C, 
 hipError_t launch_zero_border(void* buf, int32_t N, int32_t H, int32_t W, int32_t C,
                               hipStream_t s);
 
+// While alive (and `on`), this thread's stream-capture mode is relaxed, so
+// that the library's own calls that are not stream work (hipEventQuery of work
+// recorded outside a capture, hipFuncSetAttribute) do not invalidate a
+// caller's global-mode capture; the kernels launched on the capturing stream
+// are captured as in any mode. The previous mode is restored on destruction.
+class RelaxedCaptureMode {
+ public:
+  explicit RelaxedCaptureMode(bool on) : on_(on) {
+    if (on_ && hipThreadExchangeStreamCaptureMode(&mode_) != hipSuccess) on_ = false;
+  }
+  ~RelaxedCaptureMode() {
+    if (on_) (void)hipThreadExchangeStreamCaptureMode(&mode_);
+  }
+  RelaxedCaptureMode(const RelaxedCaptureMode&) = delete;
+  RelaxedCaptureMode& operator=(const RelaxedCaptureMode&) = delete;
+
+ private:
+  bool on_;
+  hipStreamCaptureMode mode_ = hipStreamCaptureModeRelaxed;
+};
+
 // The no-allocation entry point's scratch: a file-scope device array of this
 // many bytes, one copy on every GPU the library's code is loaded on, held until
-// the process ends. scratch_address gives its address on `device`, which must
-// be the calling thread's current device (resolved once per device).
+// the process ends. scratch_setup resolves its address on `device` (which must
+// be the calling thread's current device) and creates the event that orders
+// its users; once per device, at engine set-up, so that the entry point's own
+// calls create nothing.
 constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(256) << 20;
-bool scratch_address(int device, void** ptr, std::string& error);
+bool scratch_setup(int device, std::string& error);
+
+// One call's use of a device's scratch, for every engine handle on that
+// device. Begin takes the device's scratch lock (held until the object goes
+// away) and orders stream s after the previous use when that was on another
+// stream; on a capturing stream, which cannot wait on an event recorded
+// outside the capture, the previous use must be over already, or Begin fails.
+// End records the use's completion on s (not under capture: a captured use
+// runs at each replay, which the caller orders).
+class ScratchUse {
+ public:
+  ScratchUse() = default;
+  ScratchUse(const ScratchUse&) = delete;
+  ScratchUse& operator=(const ScratchUse&) = delete;
+  ~ScratchUse();
+  bool Begin(int device, hipStream_t s, bool capturing, void** ptr, std::string& error);
+  bool End(std::string& error);
+
+ private:
+  void* dev_ = nullptr;
+  bool locked_ = false;
+  bool capturing_ = false;
+  hipStream_t stream_ = nullptr;
+};
 
 }  // namespace arthip

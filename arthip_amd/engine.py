@@ -221,16 +221,27 @@ class Engine:
 
     # -- diagnostics --------------------------------------------------------------
     DEBUG_POISON, DEBUG_SYNC_EACH, DEBUG_DUMP, DEBUG_UNFUSED = 1, 2, 4, 8
+    DEBUG_TRACE, DEBUG_HOST_PROFILE, DEBUG_DUMPOPS, DEBUG_PLAN = 16, 32, 64, 128
 
     def set_debug(self, flags: int = 0, dump_dir=None) -> None:
         """The reference's VSHIP_POISON / VSHIP_SYNC_EACH / VSHIP_DUMP switches
         (hip_engine.cc:1310-1349): POISON fills every activation interior with
         fp16 NaN before each run, SYNC_EACH synchronizes after every launch, DUMP
         writes each launch's inputs and output under dump_dir (first two runs),
-        UNFUSED runs every conv as its own launch (no residual-block fusion)."""
+        UNFUSED runs every conv as its own launch (no residual-block fusion).
+        Host-side lines to the engine's log (set_log): TRACE (VSHIP_TRACE),
+        HOST_PROFILE (HIP_PROFILE), DUMPOPS (HIP_DUMPOPS), PLAN (VSHIP_DEBUG)."""
         d = str(dump_dir).encode() if dump_dir is not None else None
         if self._lib.arthip_engine_set_debug(self._h, int(flags), d) != 0:
             raise EngineError(_lib.last_error() or "set_debug failed")
+
+    def set_log(self, path=None) -> None:
+        """Append the TRACE / HOST_PROFILE / DUMPOPS / PLAN lines to the file at
+        path (None: stderr, the default)."""
+        e = _err()
+        p = str(path).encode() if path is not None else None
+        if self._lib.arthip_engine_set_log(self._h, p, e, len(e)) != 0:
+            raise EngineError(_msg(e, "set_log failed"))
 
     def debug_flags(self) -> int:
         f = ctypes.c_int()

@@ -96,10 +96,19 @@ int arthip_engine_run_device(arthip_engine* eng, const void* in_dev, const int64
  *   arthip_engine_run_device (any input size, e.g. a 2x2 warm-up): that run
  *   creates the engine's stream and uploads its weights. Otherwise return 2.
  * - Every call on one GPU shares that GPU's scratch, which keeps the last
- *   call's contents (each call clears the zero padding it needs). Calls on one
- *   handle are ordered on the GPU like run_device; calls on different handles
- *   that overlap in time on one GPU race on the scratch and corrupt each
- *   other's results: callers must serialize them.
+ *   call's contents (each call clears the zero padding it needs). The calls
+ *   of every handle on one GPU are ordered on the GPU by one event per GPU,
+ *   created at engine set-up: a call whose stream differs from the last
+ *   call's waits for it. Calls on one handle are also ordered after its
+ *   run / run_device calls, like run_device.
+ * - Under HIP graph capture (the stream is capturing): the call enqueues its
+ *   launches into the graph. The handle's previous run and the GPU's previous
+ *   scratch use must have finished (synchronize before capturing), since a
+ *   captured call cannot wait on an event recorded outside the capture;
+ *   otherwise return 2. Replays of the graph are not ordered against other
+ *   calls on the handle or the scratch: the caller orders them (and must not
+ *   replay while another call that uses the scratch is in flight).
+ *   VSHIP_SYNC_EACH is refused under capture.
  * - Not profiled and not dumped (those create events and host buffers). */
 #define ARTHIP_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
 int arthip_engine_run_device_noalloc(arthip_engine* eng, const void* in_dev,
@@ -138,13 +147,36 @@ int arthip_engine_profile_read(arthip_engine* eng, int max_steps, double* total_
  *   default a 64 -> 64 conv whose output only the next 64 -> 64 conv reads
  *   runs fused with it (arthip_conv3x3_block_f16_nhwc), which agrees with
  *   separate launches to fp16 rounding. Changing it drops the cached plans.
+ * Host-side lines, written to the engine's log (stderr, or the file given to
+ * arthip_engine_set_log):
+ * - TRACE (VSHIP_TRACE=1; hip_engine.cc:1280-1298,1421-1425,1619): per run
+ *   "[run] enter #R <entry> in=<ptr>", "[run] built #R" once the plan is
+ *   ready, "[run] #R opK <step>" after each launch, then "[run] done #R
+ *   out=<ptr>" or "[run] fail #R: <error>".
+ * - HOST_PROFILE (HIP_PROFILE=1; hip_graph.cc:1213-1447): host time spans of
+ *   each run. arthip_engine_run: "[hipprof] build= memin= launch=
+ *   readback+wait=" and "[hipprof] memout= total=" (ms); the device entry
+ *   points: "[hipprof] build= launch= total=" (enqueue only).
+ * - DUMPOPS (HIP_DUMPOPS set to any value; hip_graph.cc:1366-1373): per launch
+ *   "[dump] op K <step> in=<buf>(<ptr>,<MB>MB) ... out=<buf>(<ptr>,<MB>MB)",
+ *   buffers by plan index, or input / output for the boundary tensors.
+ * - PLAN (VSHIP_DEBUG=1; hip_engine.cc:1167-1184): each new plan's launch list,
+ *   "[vship] plan for [N,C,H,W]: ..." and one "[vship] stepK" line per launch.
  * Returns 1 on an unknown flag or DUMP without a directory. */
 #define ARTHIP_DEBUG_POISON 1
 #define ARTHIP_DEBUG_SYNC_EACH 2
 #define ARTHIP_DEBUG_DUMP 4
 #define ARTHIP_DEBUG_UNFUSED 8
+#define ARTHIP_DEBUG_TRACE 16
+#define ARTHIP_DEBUG_HOST_PROFILE 32
+#define ARTHIP_DEBUG_DUMPOPS 64
+#define ARTHIP_DEBUG_PLAN 128
 int arthip_engine_set_debug(arthip_engine* eng, int flags, const char* dump_dir);
 int arthip_engine_get_debug(const arthip_engine* eng, int* flags);
+/* Log of the TRACE / HOST_PROFILE / DUMPOPS / PLAN lines: appended to the file
+ * at path, or stderr for NULL or "" (the default, as the reference writes
+ * them). Returns 1 if the file cannot be opened (the log is unchanged). */
+int arthip_engine_set_log(arthip_engine* eng, const char* path, char* err, int errlen);
 
 /* ------------------------------------------------------------------------ */
 /* ONNX Runtime execution provider: partitioning and compile                  */

@@ -195,6 +195,17 @@ def test_engine_fused_blocks_vs_oracle(builder, shape):
     assert ef <= 1.25 * ep + 1e-4, (ef, ep)
 
 
+#: Per-element difference between the fused and unfused 1080p frames. R8F64
+#: (outputs up to ~370): the largest measures 1.125, bound 1.7. The shipped
+#: architecture's outputs are clipped to [0, 1] from pre-clip values in the
+#: hundreds, so near the clip edges a rounding difference can move an output
+#: by the whole range (max-abs 1 is measured): there the bound is on the share
+#: of elements that differ by more than 0.05, which measures 0.30 % (0.11 % by
+#: more than 0.25); bound 0.45 %.
+FUSED_VS_UNFUSED_MAX_ABS = {"r8f64": 1.7}
+FUSED_VS_UNFUSED_FAR = {"shipped_like": (0.05, 0.0045)}  # (threshold, largest share)
+
+
 @pytest.mark.parametrize("builder", [models.r8f64, models.shipped_like],
                          ids=["r8f64", "shipped_like"])
 def test_engine_fused_blocks_1080p(builder):
@@ -207,8 +218,18 @@ def test_engine_fused_blocks_1080p(builder):
     x = models.synthetic_input((1, 1, 1080, 1920), seed=9)
     fused, plain = _fused_and_plain(spec, x)
     d = _rel_rms(fused, plain)
-    print(spec.name, "1080p fused vs unfused rel RMS %.3g" % d)
+    diff = np.abs(np.asarray(fused, np.float64) - np.asarray(plain, np.float64))
+    shares = {t: float((diff > t).mean()) for t in (1 / 255, 0.05, 0.25)}
+    print(spec.name, "1080p fused vs unfused rel RMS %.3g, max-abs %.4g (output max %.4g), "
+          "share of elements differing by more than" % (d, diff.max(),
+                                                      np.abs(np.asarray(plain, np.float64)).max()),
+          shares)
     assert d <= (4e-3 if spec.name == "r8f64" else 3e-2), d
+    if spec.name in FUSED_VS_UNFUSED_MAX_ABS:
+        assert diff.max() <= FUSED_VS_UNFUSED_MAX_ABS[spec.name], diff.max()
+    else:
+        t, share = FUSED_VS_UNFUSED_FAR[spec.name]
+        assert float((diff > t).mean()) <= share, shares
 
 
 @pytest.mark.parametrize("builder,want", [

@@ -150,14 +150,15 @@ def test_narrow_pack_layout():
 def test_debug_switches_without_a_gpu(tmp_path, monkeypatch):
     """set_debug / get_debug and the VSHIP_* environment switches need no device."""
     from arthip_amd.engine import Engine, EngineError
-    for var in ("VSHIP_POISON", "VSHIP_SYNC_EACH", "VSHIP_DUMP"):
+    for var in ("VSHIP_POISON", "VSHIP_SYNC_EACH", "VSHIP_DUMP", "VSHIP_TRACE", "HIP_PROFILE",
+                "HIP_DUMPOPS", "VSHIP_DEBUG"):
         monkeypatch.delenv(var, raising=False)
     e = Engine(0)
     assert e.debug_flags() == 0
     e.set_debug(Engine.DEBUG_POISON | Engine.DEBUG_DUMP, tmp_path)
     assert e.debug_flags() == 5
     with pytest.raises(EngineError):
-        e.set_debug(16)
+        e.set_debug(256)
     with pytest.raises(EngineError):
         e.set_debug(Engine.DEBUG_DUMP)  # no directory
     e.set_debug(0)
@@ -220,3 +221,48 @@ def test_head_boundary_input_rule(tmp_path):
     out = subprocess.run([str(exe)] + args, check=True, capture_output=True, text=True).stdout
     got = [int(v) for v in out.split()]
     assert got == [want for _, want in cases], list(zip(cases, got))
+
+
+def test_host_log_switches_without_a_gpu(tmp_path, monkeypatch):
+    """The reference's host-side switches VSHIP_TRACE, HIP_PROFILE, HIP_DUMPOPS
+    (set to anything) and VSHIP_DEBUG become engine flags at creation; set_debug
+    takes them too. Without a GPU a run fails at device set-up, and the trace
+    still brackets it: an enter line, then a fail line carrying the error."""
+    from arthip_amd import models
+    from arthip_amd.engine import Engine, EngineError
+    for var in ("VSHIP_POISON", "VSHIP_SYNC_EACH", "VSHIP_DUMP"):
+        monkeypatch.delenv(var, raising=False)
+    monkeypatch.setenv("VSHIP_TRACE", "1")
+    monkeypatch.setenv("HIP_PROFILE", "1")
+    monkeypatch.setenv("HIP_DUMPOPS", "yes")
+    monkeypatch.setenv("VSHIP_DEBUG", "1")
+    with Engine(0) as e:
+        assert e.debug_flags() == 16 | 32 | 64 | 128
+    monkeypatch.setenv("VSHIP_TRACE", "0")
+    monkeypatch.setenv("HIP_PROFILE", "0")
+    monkeypatch.delenv("HIP_DUMPOPS")
+    monkeypatch.setenv("VSHIP_DEBUG", "")
+    with Engine(0) as e:
+        assert e.debug_flags() == 0
+        e.set_debug(Engine.DEBUG_TRACE | Engine.DEBUG_HOST_PROFILE | Engine.DEBUG_DUMPOPS
+                    | Engine.DEBUG_PLAN)
+        assert e.debug_flags() == 240
+        with pytest.raises(EngineError, match="cannot open log file"):
+            e.set_log(tmp_path / "no_such_dir" / "log.txt")
+        log = tmp_path / "engine.log"
+        e.set_log(log)
+        e.build(models.c4f32(seed=0))
+        try:
+            import torch
+            has_gpu = torch.cuda.is_available()
+        except ImportError:
+            has_gpu = False
+        if has_gpu:
+            return
+        x = models.synthetic_input((1, 1, 8, 8), seed=1)
+        with pytest.raises(EngineError) as err:
+            e.run(x)
+    lines = log.read_text().splitlines()
+    assert lines[0].startswith("[run] enter #1 run in=0x"), lines
+    assert lines[-1].startswith("[run] fail #1: "), lines
+    assert str(err.value).split(":")[0] in lines[-1], (err.value, lines)

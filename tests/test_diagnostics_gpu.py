@@ -123,3 +123,77 @@ def test_dump_writes_every_launch_of_the_first_two_runs(tmp_path, fused):
             assert np.isfinite(a[:, 1:21, 1:29, :]).all(), f"op{k}: non-finite interior"
             nxt = (tmp_path / f"run{run}_op{k + 1:02d}_in0.bin").read_bytes()
             assert nxt == a.tobytes(), f"op{k + 1} input differs from op{k} output"
+
+
+def test_host_log_lines(tmp_path):
+    """TRACE, HOST_PROFILE, DUMPOPS and PLAN (the reference's VSHIP_TRACE,
+    HIP_PROFILE, HIP_DUMPOPS and VSHIP_DEBUG) write their lines to the engine's
+    log: the plan once per new shape, per run an enter / built / one line per
+    launch / done sequence, one op-dump line per launch naming its buffers, and
+    the host time spans; the output does not change."""
+    import re
+
+    spec = models.r8f64(seed=0)
+    x = models.synthetic_input((1, 1, 60, 90), seed=2)
+    log = tmp_path / "engine.log"
+    with Engine(0) as e:
+        e.build(spec)
+        want = e.run(x)
+        e.set_debug(Engine.DEBUG_TRACE | Engine.DEBUG_HOST_PROFILE | Engine.DEBUG_DUMPOPS
+                    | Engine.DEBUG_PLAN)
+        e.set_log(log)
+        y1 = e.run(x)  # same shape: planned already, no plan lines
+        y2 = e.run(np.ascontiguousarray(x[:, :, :40, :70]))  # a new plan
+        e.set_debug(0)
+        e.set_log(None)
+    np.testing.assert_array_equal(y1.view(np.uint16), want.view(np.uint16))
+    lines = log.read_text().splitlines()
+    steps = [l for l in lines if l.startswith("[vship] step")]
+    assert len(steps) == 10, lines  # head, 8 blocks, tail
+    assert sum(l.startswith("[vship] plan for [1,1,40,70]: 10 launches") for l in lines) == 1
+    for r, out_shape in ((1, y1), (2, y2)):
+        mine = [l for l in lines if re.match(r"\[run\] (enter |built |done |fail )?#%d\b" % r, l)]
+        assert mine[0].startswith("[run] enter #%d run in=0x" % r), mine
+        assert mine[1] == "[run] built #%d" % r, mine
+        ops = mine[2:-1]
+        assert [l.split()[2] for l in ops] == ["op%d" % k for k in range(10)], ops
+        assert "direct_conv" in ops[0] and all("winograd_block" in l for l in ops[1:9])
+        assert "+dts2" in ops[9], ops
+        assert mine[-1].startswith("[run] done #%d out=0x" % r), mine
+    dumps = [l for l in lines if l.startswith("[dump] op ")]
+    assert len(dumps) == 20, dumps
+    assert all(" in=" in l and " out=" in l for l in dumps)
+    assert dumps[0].split(" in=")[1].startswith("input(0x"), dumps[0]  # the head reads the input
+    assert dumps[9].split(" out=")[1].startswith("output(0x"), dumps[9]  # the tail writes the output
+    prof = [l for l in lines if l.startswith("[hipprof]")]
+    assert len(prof) == 4, prof
+    assert re.match(r"\[hipprof\] build=[0-9.]+ms memin=[0-9.]+ms launch=[0-9.]+ms "
+                    r"readback\+wait=[0-9.]+ms$", prof[0]), prof
+    assert re.match(r"\[hipprof\] memout=[0-9.]+ms total=[0-9.]+ms$", prof[1]), prof
+
+
+def test_vs_trace_lines(capfd, monkeypatch):
+    """VSHIP_TRACE=1 at filter creation: an enter and a leave line on stderr
+    around every frame, naming the pool's engine (vs_hip.cpp:239-246)."""
+    import re
+
+    from arthip_amd import vs
+
+    monkeypatch.setenv("VSHIP_TRACE", "1")
+    frame = models.synthetic_input((1, 1, 24, 40), seed=3)[0, 0]
+    with vs.Model("GRAYH", 40, 24, op.encode_model(models.c4f32(seed=0).model),
+                  num_streams=2) as m:
+        monkeypatch.delenv("VSHIP_TRACE")
+        capfd.readouterr()
+        for _ in range(3):
+            m.get_frame([frame])
+    err = capfd.readouterr().err.splitlines()
+    enters = [l for l in err if l.startswith("[trace] enter")]
+    leaves = [l for l in err if l.startswith("[trace] leave")]
+    assert len(enters) == 3 and len(leaves) == 3, err
+    for k, (a, b) in enumerate(zip(enters, leaves)):
+        ma = re.match(r"\[trace\] enter eng=([01]) n=(\d+) t=(\d+)$", a)
+        mb = re.match(r"\[trace\] leave eng=([01]) n=(\d+) t=(\d+)$", b)
+        assert ma and mb, (a, b)
+        assert ma.group(1) == mb.group(1) and int(ma.group(2)) == int(mb.group(2)) == k
+        assert int(mb.group(3)) >= int(ma.group(3))
