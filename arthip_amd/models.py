@@ -43,6 +43,8 @@ class ModelSpec:
     scale: int
     convs: list  # (cin, cout) per conv in execution order, for FLOP/byte counting
     skips_per_conv: list  # residual inputs fused into each conv (0, 1 or 2)
+    conv_inputs: list | None = None  # input tensor name per conv
+    skip_names: list | None = None  # residual input tensor names per conv
 
     def bytes(self) -> bytes:
         return op.encode_model(self.model)
@@ -60,6 +62,8 @@ class _Builder:
         self.inits: list[op.Tensor] = []
         self.convs: list = []
         self.skips: list = []
+        self.conv_in: list = []
+        self.skip_names: list = []
         self.k = 0
 
     def conv(self, x: str, cin: int, cout: int, act: str | None = None) -> str:
@@ -79,6 +83,8 @@ class _Builder:
                                   strides=[1, 1], dilations=[1, 1], group=1))
         self.convs.append((cin, cout))
         self.skips.append(0)
+        self.conv_in.append(x)
+        self.skip_names.append([])
         if act == "relu":
             self.nodes.append(op.node("Relu", [y], [f"relu{i}"]))
             y = f"relu{i}"
@@ -91,6 +97,7 @@ class _Builder:
     def add(self, a: str, b: str, name: str) -> str:
         self.nodes.append(op.node("Add", [a, b], [name]))
         self.skips[-1] += 1
+        self.skip_names[-1].append(b)
         return name
 
     def finish(self, x_in: str, y: str, cin: int, cout: int, out_name="y") -> op.Model:
@@ -146,7 +153,7 @@ def artcnn(blocks: int, filters: int, *, convs_per_block: int = 2, act: str = "r
         b.nodes.append(op.node("Clip", [t, "clip_lo", "clip_hi"], ["clipped"]))
         t = "clipped"
     model = b.finish(x, t, in_ch, out_ch)
-    return ModelSpec(model, name, in_ch, out_ch, scale, b.convs, b.skips)
+    return ModelSpec(model, name, in_ch, out_ch, scale, b.convs, b.skips, b.conv_in, b.skip_names)
 
 
 def c4f32(seed: int = 0) -> ModelSpec:
@@ -157,14 +164,14 @@ def c4f32(seed: int = 0) -> ModelSpec:
     t = b.conv(t, 32, 4)
     b.nodes.append(op.node("DepthToSpace", [t], ["d2s"], blocksize=2, mode="DCR"))
     model = b.finish("x", "d2s", 1, 1)
-    return ModelSpec(model, "c4f32", 1, 1, 2, b.convs, b.skips)
+    return ModelSpec(model, "c4f32", 1, 1, 2, b.convs, b.skips, b.conv_in, b.skip_names)
 
 
 def single64(seed: int = 0) -> ModelSpec:
     b = _Builder(seed, bias="uniform")
     t = b.conv("x", 64, 64, "relu")
     model = b.finish("x", t, 64, 64)
-    return ModelSpec(model, "single64", 64, 64, 1, b.convs, b.skips)
+    return ModelSpec(model, "single64", 64, 64, 1, b.convs, b.skips, b.conv_in, b.skip_names)
 
 
 def r8f64(seed: int = 0, **kw) -> ModelSpec:
@@ -251,4 +258,5 @@ def widen_to_fp32(spec: ModelSpec, name: str | None = None) -> ModelSpec:
                      outputs=[op.value_info(go.name, op.FLOAT, go.shape)])
     model = op.Model(graph=graph, opset_imports=list(spec.model.opset_imports))
     return ModelSpec(model, name or spec.name + "_fp32", spec.in_channels, spec.out_channels,
-                     spec.scale, list(spec.convs), list(spec.skips_per_conv))
+                     spec.scale, list(spec.convs), list(spec.skips_per_conv),
+                     spec.conv_inputs, spec.skip_names)

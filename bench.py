@@ -73,6 +73,8 @@ def parse():
                         "shipped_like 56, r16f96 16, single64 and c4f32 the whole frame)")
     p.add_argument("--no-profile", action="store_true",
                    help="skip the per-launch event timing (roofline becomes null)")
+    p.add_argument("--no-e2e", action="store_true",
+                   help="skip the host-buffer (PCIe-inclusive) rates (end_to_end becomes null)")
     p.add_argument("--host-path", type=int, default=0, metavar="STREAMS",
                    help="instead of the device-resident bench, time the VapourSynth filter "
                         "path (host planes in and out, PCIe included) with STREAMS engines and "
@@ -253,26 +255,22 @@ def cpu_library(spec, x_full, rows: int) -> dict | None:
     }
 
 
-def host_path(args) -> int:
-    """Frames/s through arthip_vs_model_get_frame: fp16 planes in host memory
-    (GRAYH), copied to pinned staging, uploaded, run, downloaded and copied
-    into the caller's output plane, from several threads over an engine pool."""
+def host_path_wall(spec, h: int, w: int, streams: int, warmup: int, steps: int) -> float:
+    """Seconds for `steps` frames through arthip_vs_model_get_frame: fp16 planes
+    in host memory (GRAYH), copied to pinned staging, uploaded, run, downloaded
+    and copied into the caller's output plane, from streams + 1 threads over a
+    pool of `streams` engines."""
     import threading
 
     from arthip_amd import models, vs
     from arthip_amd import onnx_proto as op
 
-    builder = {"r8f64": models.r8f64, "r16f96": models.r16f96, "c4f32": models.c4f32,
-               "shipped_like": models.shipped_like}[args.model]
-    spec = builder(seed=0)
-    h, w = args.height, args.width
     frame = models.synthetic_input((1, 1, h, w), seed=1)[0, 0]
-    streams = args.host_path
     threads = streams + 1
     with vs.Model("GRAYH", w, h, op.encode_model(spec.model), num_streams=streams) as m:
-        for _ in range(max(args.warmup, threads)):
+        for _ in range(max(warmup, threads)):
             m.get_frame([frame])
-        counter = iter(range(args.steps))
+        counter = iter(range(steps))
         lock = threading.Lock()
 
         def work():
@@ -288,16 +286,48 @@ def host_path(args) -> int:
             t.start()
         for t in pool:
             t.join()
-        wall = time.perf_counter() - t0
+        return time.perf_counter() - t0
+
+
+def host_path(args) -> int:
+    """The VapourSynth filter path's frame rate as a JSON line of its own."""
+    from arthip_amd import models
+
+    builder = {"r8f64": models.r8f64, "r16f96": models.r16f96, "c4f32": models.c4f32,
+               "shipped_like": models.shipped_like}[args.model]
+    spec = builder(seed=0)
+    h, w = args.height, args.width
+    streams = args.host_path
+    wall = host_path_wall(spec, h, w, streams, args.warmup, args.steps)
     print(json.dumps({
         "metric": f"frames/sec @{w}x{h} {spec.name} through the VapourSynth filter path "
                   "(host planes in and out, PCIe included)",
         "value": round(args.steps / wall, 3), "unit": "frames/s", "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(1000 * wall / args.steps, 4),
-        "num_streams": streams, "threads": threads, "clip_format": "GRAYH",
+        "num_streams": streams, "threads": streams + 1, "clip_format": "GRAYH",
         "data": "synthetic (seeded He-normal fp16 weights, uniform[0,1) luma)",
     }), flush=True)
     return 0
+
+
+def end_to_end(spec, eng, x_host, frames: int) -> dict:
+    """Frame rates with host buffers (PCIe included), beside the device-resident
+    value: the engine's own Run (pinned staging, upload, run, download, one
+    engine, synchronous) and the VapourSynth filter path with two engines and
+    three caller threads (transfers of one frame overlap another's run)."""
+    t0 = time.perf_counter()
+    for _ in range(frames):
+        eng.run(x_host)
+    sync_fps = frames / (time.perf_counter() - t0)
+    n, _, h, w = x_host.shape
+    out = {"engine_run_fps": round(n * sync_fps, 3),
+           "engine_run_what": f"arthip_engine_run host->host, one engine, {frames} frames"}
+    if spec.in_channels == 1 and n == 1:
+        wall = host_path_wall(spec, h, w, 2, 3, frames)
+        out["vs_filter_fps"] = round(frames / wall, 3)
+        out["vs_filter_what"] = (f"VapourSynth filter core (GRAYH planes in host memory), "
+                                 f"num_streams=2, 3 caller threads, {frames} frames")
+    return out
 
 
 def stream_copy_gbs(nbytes: int, reps: int = 20) -> float:
@@ -336,9 +366,11 @@ def profile_launches(key: str):
 def launch_work(spec, steps, px: int):
     """Algorithmic bytes and flops of each engine launch of one frame, in launch
     order (the engine's profile step names): a conv step takes the next conv of
-    the model, a fused block step the next two. Bytes: every tensor the launch
-    reads or writes, fp16, once (input, residual inputs, output; the boundary
-    input / output of the head / tail at their own sizes), plus fp16 weights."""
+    the model, a fused block step the next two. Bytes: every distinct tensor the
+    launch reads or writes, fp16, once (input, residual inputs, output; the
+    boundary input / output of the head / tail at their own sizes), plus fp16
+    weights. A fused block whose residual input is its own input tensor (every
+    R8F64 block) reads that tensor once: 531 MB at 1080p, not 796."""
     convs = list(zip(spec.convs, spec.skips_per_conv))
     ci = 0
     out = []
@@ -346,6 +378,9 @@ def launch_work(spec, steps, px: int):
         if name.startswith("winograd_block"):
             (c1, m1), _ = convs[ci]
             (c2, m2), nsk = convs[ci + 1]
+            if spec.conv_inputs is not None:
+                block_in = spec.conv_inputs[ci]
+                nsk = sum(1 for t in spec.skip_names[ci + 1] if t != block_in)
             ci += 2
             b = 2.0 * px * (c1 + m2 * (1 + nsk)) + 18.0 * (c1 * m1 + c2 * m2)
             fd = 2.0 * 9 * px * (c1 * m1 + c2 * m2)
@@ -359,6 +394,25 @@ def launch_work(spec, steps, px: int):
                         "flops_wino": fd * 16 / 36 if c > 1 else fd, "convs": 1})
         else:
             out.append(None)
+    return out
+
+
+def frame_bytes(spec, work, n, h, w, oshape, roofline) -> dict:
+    """HBM bytes of one frame three ways: every conv launched alone
+    (layer-at-a-time), the launches as the engine runs them (each distinct tensor
+    a launch touches once), and the fused lower bound (the frame's boundary
+    input and output plus the weights: what an engine keeping every
+    intermediate on chip would move)."""
+    weights = sum(18.0 * c * m for c, m in spec.convs)
+    lower = 2.0 * n * h * w * spec.in_channels + 2.0 * oshape[0] * oshape[1] * oshape[2] * oshape[3] + weights
+    out = {"layer_at_a_time": round(work["bytes"]), "fused_lower_bound": round(lower)}
+    if roofline:
+        per_launch = sum(k["alg_bytes"] * k["launches_per_frame"] for k in roofline["kernels"])
+        out["as_launched"] = round(per_launch)
+        meas = [k.get("hbm_bytes_measured") for k in roofline["kernels"]]
+        if all(m is not None for m in meas):
+            out["measured"] = round(sum(m * k["launches_per_frame"]
+                                        for m, k in zip(meas, roofline["kernels"])))
     return out
 
 
@@ -637,6 +691,9 @@ def main() -> int:
                 "kernels": table,
             }
 
+    # Host-buffer rates (PCIe included): reported beside the device-resident value.
+    e2e = end_to_end(spec, eng, x_host, max(4, min(args.steps, 40))) if not args.no_e2e else None
+
     rows = args.cpu_rows
     if rows < 0:
         rows = {"r8f64": 80, "shipped_like": 56, "r16f96": 16}.get(args.model, h)
@@ -671,6 +728,8 @@ def main() -> int:
         "tflops_direct_equiv": round(tflops_direct, 2),
         "tflops_winograd": round(work["flops_wino"] * fps / n / 1e12, 2),
         "hbm_gbs_layer_at_a_time": round(work["bytes"] * fps / n / 1e9, 1),
+        "frame_bytes": frame_bytes(spec, work, n, h, w, oshape, roofline),
+        "end_to_end": e2e,
         "wall_s": round(wall, 3),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -30,3 +30,23 @@ def test_torch_runner_matches_the_fp32_oracle(builder, hw):
     assert got.shape == want.shape
     rel = np.sqrt(np.mean((got - want) ** 2)) / np.sqrt(np.mean(want ** 2))
     assert rel < 1e-4, rel
+
+
+def test_launch_work_counts_each_distinct_tensor_once():
+    """A fused R8F64 block's residual is its own input: input + output, 531 MB at
+    1080p; the last block adds the global skip (796 MB). A shipped-architecture
+    block (the last two convs of a 3-conv block) reads its input, the block's
+    residual (another tensor) and writes its output: 796 MB."""
+    px = 1080 * 1920
+    act = 2.0 * px * 64
+    w2 = 2 * 18.0 * 64 * 64
+    r8 = models.r8f64(seed=0)
+    steps = ["direct_conv"] + ["winograd_block"] * 8 + ["winograd_conv"]
+    got = [x["bytes"] for x in bench.launch_work(r8, steps, px)]
+    assert got[1:8] == [2 * act + w2] * 7
+    assert got[8] == 3 * act + w2
+    sh = models.shipped_like(seed=0)
+    steps = ["direct_conv"] + ["winograd_conv", "winograd_block"] * 8 + ["winograd_conv"] * 2
+    got = [x["bytes"] for x in bench.launch_work(sh, steps, px)]
+    assert got[2] == 3 * act + w2
+    assert got[1] == 2 * act + 18.0 * 64 * 64
