@@ -49,7 +49,10 @@ struct Epilogue {
 
 // Winograd F(2x2,3x3) conv, C > 1 (winograd_conv in kernels.hip).
 struct WinoArgs {
-  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C]
+  // in_nchw 0: padded NHWC fp16 [N][Hp][Wp][C]; 1: the engine's NCHW fp16
+  // boundary input [N][C][H][W] (a 64 -> 64 pipe conv reading it directly).
+  const uint16_t* in;
+  int32_t in_nchw;
   const uint16_t* u;   // packed transformed filters (winograd_pack)
   Epilogue epi;
   int32_t N, H, W, C, M;
@@ -72,12 +75,12 @@ struct FastDiv {
 // ordered (n, strip of 16 tile columns, tile row) with the tile row fastest, so
 // consecutive items of a workgroup slide down one strip.
 struct StripArgs {
-  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C]
+  const uint16_t* in;  // padded NHWC fp16 [N][Hp][Wp][C] (or NCHW fp16, winograd_pipe IO bit 0)
   const uint16_t* u;   // packed transformed filters (winograd_pack)
   const float* bias;   // [C] fp32
   const uint16_t* skip0;
   const uint16_t* skip1;
-  uint16_t* out;  // padded NHWC fp16, same geometry as the input
+  uint16_t* out;  // padded NHWC fp16, same geometry as the input (or NCHW fp16, IO bit 1)
   int32_t N, H, W, Hp, Wp;
   int32_t tiles_h, tiles_w, n_strips;
   int32_t n_items;  // N * n_strips * tiles_h

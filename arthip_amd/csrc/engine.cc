@@ -486,10 +486,17 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
   // writes the padded layout on the fast body kernels instead; the tiled output
   // conversion then moves it to the boundary (the conv kernels' general
   // boundary epilogue stores one element at a time).
+  // The exception is a 64 -> 64 conv without residual inputs that the pipe
+  // kernel can store in the fp16 boundary layout itself (pipe_boundary_io).
   bool final_wide = false;
   if (final_op >= 0 && ops[final_op].kind == OpKind::Conv) {
     const Op& fo = ops[final_op];
-    final_wide = graph_.weights.at(fo.weight).dims[0] > 16 && fo.dts_b < 1 && !fo.clip;
+    const auto& dims = graph_.weights.at(fo.weight).dims;
+    final_wide = dims[0] > 16 && fo.dts_b < 1 && !fo.clip;
+    const Shape fi = shapes.at(fo.in0);
+    if (final_wide && !graph_.output_fp32 && fo.skips.empty() &&
+        pipe_boundary_io(fi.n, fi.h, fi.w, dims[1], dims[0], false))
+      final_wide = false;
   }
   const bool direct_out = final_op >= 0 && !output_read_inside && !final_wide &&
                           (ops[final_op].kind == OpKind::Conv ||
@@ -556,10 +563,12 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
 
   // Boundary input -> internal padded tensor, unless its only reader is a
   // one-channel head conv on the fast path (padded output, M % 8 == 0, no
-  // Clip or residual input): that conv reads the NCHW boundary input itself.
+  // Clip or residual input), or a 64 -> 64 conv without residual input, Clip
+  // or DepthToSpace that the pipe kernel runs on a 64-channel fp16 input
+  // (pipe_boundary_io): that conv reads the NCHW boundary input itself.
   const Shape sin = shapes.at(graph_.input_name);
   int fused_in_op = -1;
-  if (sin.c == 1 && graph_.output_name != graph_.input_name) {
+  if ((sin.c == 1 || sin.c == 64) && graph_.output_name != graph_.input_name) {
     int readers = 0, reader = -1;
     bool other_use = false;
     for (int i = 0; i < nops; ++i) {
@@ -574,8 +583,13 @@ bool Engine::EnsurePlan(Plan& p, const int64_t in[4], std::string& error, void* 
       const Op& op = ops[reader];
       const int64_t m = graph_.weights.at(op.weight).dims[0];
       const bool to_boundary = direct_out && reader == final_op;
-      if (!to_boundary && !op.clip && op.dts_b < 1 && op.skips.empty() &&
+      const bool plain = !op.clip && op.dts_b < 1 && op.skips.empty();
+      if (sin.c == 1 && plain && !to_boundary &&
           head_reads_boundary_input(sin.n, sin.h, sin.w, m, graph_.input_fp32))
+        fused_in_op = reader;
+      // (A 64-channel conv writing the boundary does so through the same pipe.)
+      if (sin.c == 64 && plain && !graph_.input_fp32 &&
+          pipe_boundary_io(sin.n, sin.h, sin.w, sin.c, m, true))
         fused_in_op = reader;
     }
   }
@@ -914,6 +928,7 @@ bool Engine::Enqueue(const Plan& p, const void* in_dev, void* out_dev, hipStream
         } else {
           WinoArgs a{};
           a.in = static_cast<const uint16_t*>(ptr(st.in));
+          a.in_nchw = st.in == kBoundaryIn ? 1 : 0;
           a.u = static_cast<const uint16_t*>(wbufs_[st.wbuf].ptr);
           a.epi = epi;
           a.N = st.N; a.H = st.H; a.W = st.W; a.C = st.C; a.M = st.M;

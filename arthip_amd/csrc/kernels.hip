@@ -35,6 +35,7 @@
 
 #include <atomic>
 #include <cstdint>
+#include <type_traits>
 
 #include "conv_args.h"
 #include "launch.h"
@@ -707,6 +708,19 @@ winograd_strip(StripArgs a) {
 //
 // C = 96: six consumer waves (192 VGPRs of U' each) and two producer waves,
 // each transforming three (tile, 4-channel) tasks per item.
+//
+// Boundary layouts (C = M = 64 without residual inputs; IO bit 0 / bit 1):
+// the producers can read the engine's NCHW fp16 input and the consumers write
+// the NCHW fp16 output, so that a lone 64 -> 64 conv between boundary tensors
+// needs no layout passes (W % 8 == 0). NCHW input: the producers copy the
+// strip's rows into an LDS row ring (below) and repack each patch into the
+// channel-pair layout of the transform; a producer wave's lanes take tiles
+// 0-7 of four channel quads, then tiles 8-15, so that its V' writes hit
+// distinct LDS banks. NCHW output:
+// the fold stages the item channel-major ([row][channel][32 pixels], 80-byte
+// channel rows so the fold's 4-byte writes of four channel quads land on
+// distinct banks), and each consumer thread stores 8 pixels of one channel as
+// a 16-byte word.
 template <int KC>
 struct PipeL;
 template <>
@@ -747,16 +761,29 @@ struct PipeLds {
   static constexpr int NPT = 64 * (8 - NCW);  // producer threads
   static constexpr int UP = 16 * 8 * KC / NPT;  // producer tasks per thread
   static constexpr int OCH = 2 * PXS * (C / 8) / NPT;  // 16-byte output chunks per producer thread
-  static constexpr size_t lds_bytes() { return (size_t)2 * (VBUF + SBUF) * 2; }
+  // Channel-major staging of the NCHW output: [row][channel][NCS halfs].
+  static constexpr int NCS = 40;
+  static constexpr int SBUF_NCHW = 2 * C * NCS;
+  // Row ring of the NCHW input (C = 64): NSL_NCHW slots of 12 KB after the
+  // staging buffers.
+  static constexpr int NSL_NCHW = 6;
+  static constexpr size_t RING_NCHW_BYTES = (size_t)NSL_NCHW * 2 * 64 * 96;
+  static constexpr size_t lds_bytes(bool out_nchw = false, bool in_nchw = false) {
+    return (size_t)2 * (VBUF + (out_nchw ? SBUF_NCHW : SBUF)) * 2 +
+           (in_nchw ? RING_NCHW_BYTES : 0);
+  }
 };
 
-template <int KC, int ACT, int NSKIP>
+template <int KC, int ACT, int NSKIP, int IO = 0>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 winograd_pipe(StripArgs a) {
   using L = PipeLds<KC>;
   using LL = PipeL<KC>;
   constexpr int C = L::C;
   constexpr int NCW = L::NCW;
+  constexpr bool IN_NCHW = (IO & 1) != 0;
+  constexpr bool OUT_NCHW = (IO & 2) != 0;
+  static_assert(IO == 0 || (KC == 2 && NSKIP == 0), "boundary layouts: 64 channels, no residuals");
   // With two residual inputs at C = 96 the producers' 3-slot row ring and
   // residual registers exceed 256 VGPRs and spill; a 2-slot ring does not
   // (1080p: 378 -> 327 us). Shallower rings elsewhere measured slower.
@@ -764,7 +791,7 @@ winograd_pipe(StripArgs a) {
   constexpr int UP = L::UP;
   constexpr int WPS = L::WPS;
   constexpr int VBUF = L::VBUF;
-  constexpr int SBUF = L::SBUF;
+  constexpr int SBUF = OUT_NCHW ? L::SBUF_NCHW : L::SBUF;
   constexpr int PXS = L::PXS;
   constexpr int GR = C / 8;  // 16-byte groups per pixel
   constexpr int QUADS = C / 4;
@@ -832,6 +859,25 @@ winograd_pipe(StripArgs a) {
     auto store_item = [&](int item, bool live, int SB) {
       int n, s, th;
       decode(item, n, s, th);
+      if constexpr (OUT_NCHW) {
+        // Thread: channel tid / 4, pixels 8 (tid % 4) .. + 7 of the item's
+        // strip, in both rows; the row in the scalar offset.
+        const uint32_t plane = (uint32_t)a.H * (uint32_t)a.W * 2;
+        const char* ob = reinterpret_cast<const char*>(a.out) + (int64_t)n * C * plane;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)ob, (short)0, (int)(C * plane), 0x00020000);
+        const int ch = tid >> 2, k = tid & 3;
+        const int x = PXS * s + 8 * k;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const h8 v = *reinterpret_cast<const h8*>(stg + SB * SBUF + (r * C + ch) * L::NCS + 8 * k);
+          const bool ok = live && x < a.W && 2 * th + r < a.H;
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u4, v), rs, ok ? (uint32_t)ch * plane + (uint32_t)x * 2 : kOob,
+              (uint32_t)(2 * th + r) * (uint32_t)a.W * 2, kNonTemporal);
+        }
+        return;
+      }
       const int64_t pix0 = ((int64_t)n * a.Hp + 2 * th + 1) * a.Wp + PXS * s + 1;
       char* ob = reinterpret_cast<char*>(a.out) + pix0 * PX;
       const __amdgpu_buffer_rsrc_t rs =
@@ -896,6 +942,18 @@ winograd_pipe(StripArgs a) {
       // With producer stores the activation is theirs (on the rounded value,
       // the same arithmetic).
       constexpr int FA = PS ? 0 : ACT;
+      if constexpr (OUT_NCHW) {
+        // Channel-major: pixels 2 tcol and 2 tcol + 1 of channel ch0 + e, per row.
+        const h4 a0 = strip_act4<FA>(y00), a1 = strip_act4<FA>(y01);
+        const h4 b0 = strip_act4<FA>(y10), b1 = strip_act4<FA>(y11);
+        _Float16* sc = stg + BUF * SBUF + ch0 * L::NCS + 2 * tcol;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          *reinterpret_cast<h2*>(sc + e * L::NCS) = h2{a0[e], a1[e]};
+          *reinterpret_cast<h2*>(sc + (C + e) * L::NCS) = h2{b0[e], b1[e]};
+        }
+        return;
+      }
       _Float16* sw = stg + BUF * SBUF + sw0;
       *reinterpret_cast<h4*>(sw) = strip_act4<FA>(y00);
       *reinterpret_cast<h4*>(sw + C) = strip_act4<FA>(y01);
@@ -934,8 +992,15 @@ winograd_pipe(StripArgs a) {
 #pragma unroll
   for (int v = 0; v < UP; ++v) {
     const int f = ptid + L::NPT * v;
-    tt[v] = f / QUADS;
-    tq4[v] = (uint32_t)(4 * (f - tt[v] * QUADS));
+    if constexpr (IN_NCHW) {
+      // Lane l of producer wave w: tile (l & 7) + 8 (l >> 5), quad 4 w + ((l >> 3) & 3).
+      const int l = ptid & 63;
+      tt[v] = (l & 7) + 8 * (l >> 5);
+      tq4[v] = (uint32_t)(4 * (4 * (ptid >> 6) + ((l >> 3) & 3)));
+    } else {
+      tt[v] = f / QUADS;
+      tq4[v] = (uint32_t)(4 * (f - tt[v] * QUADS));
+    }
     vw0[v] = vlds + LL::at(tt[v], (int)tq4[v]);
   }
   int n, s, th;  // the item being transformed
@@ -1021,6 +1086,107 @@ winograd_pipe(StripArgs a) {
     }
   };
 
+  if constexpr (IN_NCHW) {
+    // NCHW boundary input through an LDS row ring: slot m % NSL holds image
+    // rows 2 m - 1 and 2 m of the strip, 48 pixels from 32 s - 8 (16-byte
+    // aligned; the patches use 32 s - 1 .. 32 s + 32). Each producer wave
+    // copies the rows of its own 16 channels (the ones its lanes transform)
+    // with three 16-byte buffer -> LDS loads per row pair (out-of-image
+    // chunks read as zero), and reads only what it copied: no barrier orders
+    // the ring, only the wave's own load count. Within a wave's region a
+    // channel row (96 bytes) sits at position p = 2 j + 8 (c & 1) + (c >> 1)
+    // for quad j, channel c of the quad, so that each dword read of the
+    // transform (one row and channel, 16 tiles x 4 quads) hits 64 distinct
+    // banks. Row pair m + 4 is requested while pairs m and m + 1 are read.
+    constexpr int NSL = L::NSL_NCHW;
+    constexpr int RP = 24;                // dwords per channel row
+    constexpr int WREG = 2 * 16 * RP;     // dwords of one wave's region per slot
+    constexpr int SLOT = 4 * WREG;        // dwords per slot
+    constexpr int AHEAD = NSL - 2;        // row pairs requested ahead of the first read
+    uint32_t* const ring = reinterpret_cast<uint32_t*>(stg + 2 * SBUF);
+    const uint32_t plane = (uint32_t)a.H * (uint32_t)a.W * 2;
+    const int pw = wave - NCW;  // uniform (ptid >> 6)
+    const int l = ptid & 63;
+    const int jq = (l >> 3) & 3;
+    // The three copies of lane l: chunk q = 64 i + l of the wave's region,
+    // row r = q / 96, position p = (q / 6) % 16, 16-byte chunk k = q % 6.
+    int d_row[3], d_k[3];
+    uint32_t d_ch[3], d_base[3];
+    bool d_ok[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int q = 64 * i + l;
+      const int pp = (q / 6) % 16;
+      const int c = ((pp & 1) << 1) | ((pp >> 3) & 1);
+      const int j = (pp >> 1) & 3;
+      d_row[i] = q / 96;
+      d_k[i] = q % 6;
+      d_ch[i] = (uint32_t)(16 * pw + 4 * j + c) * plane;
+    }
+    __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, 0, 0x00020000);
+    auto issue = [&](int pair) {
+      const uint32_t dst = lds_byte_addr(ring + (pair % NSL) * SLOT + pw * WREG);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int y = 2 * pair - 1 + d_row[i];
+        const bool ok = d_ok[i] && y >= 0 && y < a.H;
+        dma16_buf(dst + 1024 * i, rs, ok ? d_base[i] + (uint32_t)y * (uint32_t)a.W * 2 : kOob);
+      }
+    };
+    // Dword offsets of this lane's reads in a slot: row r, channel c of its quad.
+    auto rd = [&](int r, int c) { return pw * WREG + (r * 16 + 2 * jq + 8 * (c & 1) + (c >> 1)) * RP + 3 + tt[0]; };
+    for (int it = begin; it < end;) {
+      decode(it, n, s, th);
+      const int len = min(end - it, a.tiles_h - th);
+      const char* ib = reinterpret_cast<const char*>(a.in) + (int64_t)n * C * plane;
+      rs = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, (int)(C * plane), 0x00020000);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int x = PXS * s - 8 + 8 * d_k[i];
+        d_ok[i] = x >= 0 && x < a.W;
+        d_base[i] = d_ch[i] + (uint32_t)x * 2;
+      }
+      for (int m = 0; m < AHEAD; ++m) issue(th + m);
+      for (int k = 0; k < len; ++k) {
+        issue(th + AHEAD);
+        wait_vmcnt<3 * (AHEAD - 1)>();  // row pairs th and th + 1 have landed
+        const uint32_t* sa = ring + (th % NSL) * SLOT;
+        const uint32_t* sb = ring + ((th + 1) % NSL) * SLOT;
+        h2 top[16], bot[16];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          const uint32_t* sl = pr < 2 ? sa : sb;
+          uint32_t x[4][3];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int d = 0; d < 3; ++d) x[c][d] = sl[rd(pr & 1, c) + d];
+          // Column j of the patch is pixel pair (j + 1) / 2, half (j + 1) % 2;
+          // element 2 (4 r + j) + e holds channels 2 e and 2 e + 1.
+          h2* row = (pr < 2 ? top : bot) + 8 * (pr & 1);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int d = (j + 1) >> 1;
+              const uint32_t sel = ((j + 1) & 1) ? 0x07060302u : 0x05040100u;
+              row[2 * j + e] =
+                  __builtin_bit_cast(h2, __builtin_amdgcn_perm(x[2 * e + 1][d], x[2 * e][d], sel));
+            }
+        }
+        v_transform<WPS>(vw0[0] + par * VBUF, top, bot);
+        ++th;
+        par ^= 1;
+        lds_sync();
+      }
+      wait_vmcnt<0>();  // the copies requested past the run have landed
+      it += len;
+    }
+    lds_sync();  // step K: the consumers fold item K-1
+    lds_sync();  // step K + 1: they store it
+    return;
+  }
+
   auto step = [&](h2 (&top)[UP][16], h2 (&bot)[UP][16]) {
     if constexpr (PS) {
       store_item(begin + js - 2, js >= 2, par);  // item j-2 sits in buffer j & 1
@@ -1081,9 +1247,6 @@ winograd_pipe(StripArgs a) {
   }
 }
 
-__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
-}
 
 // One 16-byte-per-lane global -> LDS copy: lane l of the wave writes LDS bytes
 // [m0 + 16 l, m0 + 16 l + 16) from gbase + voff. Inline assembly, so the
@@ -1098,14 +1261,6 @@ __device__ __forceinline__ void dma16(uint32_t m0, const char* gbase, uint32_t v
       : "memory");
 }
 
-// Waits until at most N of this wave's vector-memory instructions are
-// outstanding (they complete in issue order). Inline assembly with a memory
-// clobber, so that the compiler moves no memory access across it.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
 
 // ---------------------------------------------------------------------------
 // Direct 3x3 conv on MFMA for narrow outputs (M <= 16), boundary layout
@@ -2470,20 +2625,45 @@ bool strip_eligible(const WinoArgs& a) {
   return a.C == 32 || a.C == 64 || a.C == 96;
 }
 
-template <int KC, int NSKIP>
+template <int KC, int NSKIP, int IO = 0>
 hipError_t launch_pipe(const StripArgs& a, int act, hipStream_t s) {
-  StripKernel pf = act == kActRelu   ? winograd_pipe<KC, kActRelu, NSKIP>
-                   : act == kActSilu ? winograd_pipe<KC, kActSilu, NSKIP>
-                                     : winograd_pipe<KC, kActNone, NSKIP>;
-  const size_t lds = PipeLds<KC>::lds_bytes();
+  StripKernel pf = act == kActRelu   ? winograd_pipe<KC, kActRelu, NSKIP, IO>
+                   : act == kActSilu ? winograd_pipe<KC, kActSilu, NSKIP, IO>
+                                     : winograd_pipe<KC, kActNone, NSKIP, IO>;
+  const size_t lds = PipeLds<KC>::lds_bytes((IO & 2) != 0, (IO & 1) != 0);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pf),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   int64_t grid = cu_count();  // one 512-thread workgroup per CU
   if (grid > a.n_items) grid = a.n_items;
+  if (IO != 0) {
+    // NCHW rows are 64 separate planes: every workgroup takes the same share
+    // of one strip's rows (a multiple of the strip count, and of 8 for the
+    // XCD mapping), so that all of them walk the same image rows together
+    // and each plane row is read across the image at once.
+    const int64_t per = (int64_t)a.N * a.n_strips;
+    for (int64_t q = grid / per; q >= 1; --q)
+      if ((per * q) % 8 == 0 && per * q <= a.n_items) {
+        grid = per * q;
+        break;
+      }
+  }
   grid = (grid + 7) / 8 * 8;
   hipLaunchKernelGGL(pf, dim3((unsigned)grid), dim3(512), lds, s, a);
   return hipGetLastError();
+}
+
+// The 64 -> 64 pipe with an NCHW fp16 boundary input and / or output
+// (pipe_boundary_io): no residual inputs, no Clip, no DepthToSpace.
+bool pipe_boundary_eligible(const WinoArgs& a) {
+  const bool nchw_out = a.epi.out_kind == kOutNchwF16;
+  if (!a.in_nchw && !nchw_out) return false;
+  if (a.epi.out_kind != kOutPadded && !nchw_out) return false;
+  if (a.epi.dts_b >= 2 || a.epi.do_clip || a.epi.skip0 != nullptr || a.epi.skip1 != nullptr)
+    return false;
+  if (a.epi.act != kActNone && a.epi.act != kActRelu && a.epi.act != kActSilu) return false;
+  return (!a.in_nchw || pipe_boundary_io(a.N, a.H, a.W, a.C, a.M, true)) &&
+         (!nchw_out || pipe_boundary_io(a.N, a.H, a.W, a.C, a.M, false));
 }
 
 hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
@@ -2509,6 +2689,15 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
   a.fd_tiles_h = make_fastdiv((uint32_t)a.tiles_h);
   a.fd_strips = make_fastdiv((uint32_t)a.n_strips);
   const int kc = w.C / 32;
+  const int io = (w.in_nchw ? 1 : 0) | (w.epi.out_kind == kOutNchwF16 ? 2 : 0);
+  if (io != 0) {
+    if (!pipe_boundary_eligible(w)) return hipErrorInvalidValue;
+    switch (io) {
+      case 1: return launch_pipe<2, 0, 1>(a, w.epi.act, s);
+      case 2: return launch_pipe<2, 0, 2>(a, w.epi.act, s);
+      default: return launch_pipe<2, 0, 3>(a, w.epi.act, s);
+    }
+  }
   // 64 channels with residual inputs stay on winograd_strip (it runs at the
   // streaming rate there).
   if (nskip == 0 && kc == 2) return launch_pipe<2, 0>(a, w.epi.act, s);
@@ -2623,6 +2812,10 @@ hipError_t launch_narrow(const WinoArgs& w, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_winograd(WinoArgs a, hipStream_t s) {
+  // An NCHW boundary input only the 64 -> 64 pipe reads (refused otherwise);
+  // an NCHW fp16 output it writes when it can (else the general epilogue).
+  if (a.in_nchw) return pipe_boundary_eligible(a) ? launch_strip(a, s) : hipErrorInvalidValue;
+  if (a.epi.out_kind == kOutNchwF16 && pipe_boundary_eligible(a)) return launch_strip(a, s);
   if (narrow_launch_eligible(a)) return launch_narrow(a, s);
   if (strip_eligible(a)) return launch_strip(a, s);
   const WinoGeom g = winograd_geom(a.C, a.M);

@@ -160,6 +160,34 @@ __device__ __forceinline__ h4 strip_act4(f4 y) {
   return r;
 }
 
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// One 16-byte-per-lane buffer -> LDS copy: lane l of the wave writes LDS bytes
+// [m0 + 16 l, m0 + 16 l + 16) from the buffer resource at byte voff; an offset
+// past the resource's size copies zeros. Inline assembly, so the compiler
+// neither tracks it nor inserts waits for it; the kernels count it.
+__device__ __forceinline__ void dma16_buf(uint32_t m0, __amdgpu_buffer_rsrc_t rs, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(m0), "v"(voff), "s"(rs)
+      : "memory");
+}
+
+// Waits until at most N of this wave's vector-memory instructions are
+// outstanding (they complete in issue order). Inline assembly with a memory
+// clobber, so that the compiler moves no memory access across it.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 template <int N>
 struct IntC {
   static constexpr int value = N;

@@ -266,3 +266,46 @@ def test_host_log_switches_without_a_gpu(tmp_path, monkeypatch):
     assert lines[0].startswith("[run] enter #1 run in=0x"), lines
     assert lines[-1].startswith("[run] fail #1: "), lines
     assert str(err.value).split(":")[0] in lines[-1], (err.value, lines)
+
+
+PIPE_RULE_PROBE = r"""
+#include <cstdio>
+#include <cstdlib>
+#include "plan_rules.h"
+int main(int argc, char** argv) {
+  for (int i = 1; i + 5 < argc; i += 6) {
+    const long long n = atoll(argv[i]), h = atoll(argv[i + 1]), w = atoll(argv[i + 2]),
+                    c = atoll(argv[i + 3]), m = atoll(argv[i + 4]), in = atoll(argv[i + 5]);
+    std::printf("%d\n", arthip::pipe_boundary_io(n, h, w, c, m, in != 0) ? 1 : 0);
+  }
+  return 0;
+}
+"""
+
+
+def test_pipe_boundary_rule(tmp_path):
+    """The planner lets a 64 -> 64 pipe conv read the NCHW fp16 boundary input
+    or write the NCHW fp16 boundary output (both need W % 8 == 0) only where
+    the kernel accepts it (one predicate, plan_rules.h): C = M = 64, one
+    image of 64 planes below 2^31 bytes. Compiled with g++ and checked at the
+    rule's boundaries."""
+    import subprocess
+    csrc = Path(__file__).resolve().parents[1] / "arthip_amd" / "csrc"
+    src = tmp_path / "probe.cc"
+    src.write_text(PIPE_RULE_PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", str(csrc), str(src), "-o", str(exe)],
+                   check=True)
+    cases = [
+        ((1, 1080, 1920, 64, 64, 1), 1), ((1, 1080, 1920, 64, 64, 0), 1),
+        ((1, 36, 70, 64, 64, 1), 0), ((1, 36, 70, 64, 64, 0), 0),
+        ((1, 35, 33, 64, 64, 1), 0), ((1, 35, 33, 64, 64, 0), 0),
+        ((1, 1080, 1920, 32, 64, 1), 0), ((1, 1080, 1920, 64, 96, 0), 0),
+        ((0, 8, 8, 64, 64, 1), 0), ((2, 2160, 3840, 64, 64, 0), 1),
+        # 64 planes of 2^24 pixels are 2^31 bytes: refused; 8 pixels less is not
+        ((1, 4096, 4096, 64, 64, 0), 0), ((1, 4096, 4088, 64, 64, 0), 1),
+    ]
+    args = [str(v) for c, _ in cases for v in c]
+    out = subprocess.run([str(exe)] + args, check=True, capture_output=True, text=True).stdout
+    got = [int(v) for v in out.split()]
+    assert got == [want for _, want in cases], list(zip(cases, got))

@@ -476,8 +476,12 @@ def test_multichannel_boundary_conversions(cin, cout, io32):
         with Engine(0) as e:
             got, names = _steps(e.build(m), x)
         got = got.astype(np.float32)
-        assert any(n.startswith("input_convert") for n in names), names
-        assert any(n.startswith("output_convert") for n in names), names
+        # A lone fp16 64 -> 64 conv reads the boundary input and writes the
+        # boundary output itself when W % 8 == 0 (test_pipe_nchw_boundary
+        # covers that path).
+        pipe = cin == cout == 64 and not io32
+        assert any(n.startswith("input_convert") for n in names) == (not pipe or w % 8 != 0), names
+        assert any(n.startswith("output_convert") for n in names) == (not pipe or w % 8 != 0), names
         want = run_model(m, x)
         floor = run_model(m, x, round_fp16=False)
         s, f = _compare(got, want), _compare(floor, want)
@@ -560,3 +564,39 @@ def test_full_frame_equals_cropped_runs(builder):
             want = full[:, :, r0 * s:r1 * s, c0 * s:c1 * s]
             np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16),
                                           err_msg=f"{spec.name} window {r0}:{r1},{c0}:{c1}")
+
+
+def _conv64(act):
+    b = models._Builder(11, "uniform")
+    y = b.conv("x", 64, 64, act)
+    m = b.finish("x", y, 64, 64)
+    init = {t.name: t.to_numpy() for t in m.graph.initializers}
+    return m, init["w0"], init["b0"]
+
+
+@pytest.mark.parametrize("act", [None, "relu", "silu"])
+@pytest.mark.parametrize("hw", [(1080, 1920), (37, 64), (36, 70), (35, 33), (2, 8), (1, 2),
+                                (9, 1000)])
+def test_pipe_nchw_boundary(act, hw):
+    """A lone fp16 64 -> 64 conv reads the NCHW boundary input in the pipe's
+    producers and stores the NCHW boundary output from its consumers (both for
+    W % 8 == 0), with no layout pass; the output equals, bit for bit, the same
+    conv on padded NHWC buffers through the kernel-level entry point (the same
+    arithmetic, other layouts), and meets the literal gate against the oracle
+    (small frames; the full 1080p single-layer frame is checked against the
+    oracle by test_single_layer_full_size)."""
+    from tests.test_conv_kernel_gpu import run_conv
+    model, w16, b16 = _conv64(act)
+    h, w = hw
+    x = models.synthetic_input((1, 64, h, w), seed=h + 7 * w, kind="normal")
+    with Engine(0) as e:
+        got, names = _steps(e.build(model), x)
+    assert any(n.startswith("input_convert") for n in names) == (w % 8 != 0), names
+    assert any(n.startswith("output_convert") for n in names) == (w % 8 != 0), names
+    code = {None: 0, "relu": 1, "silu": 2}[act]
+    ref = run_conv(x, w16, b16, act=code)
+    np.testing.assert_array_equal(got.view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    if h * w <= 40000:
+        want = run_model(model, x)
+        s = _compare(got.astype(np.float32), want)
+        assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
