@@ -483,11 +483,21 @@ def summarize_profile(args) -> int:
             L["hbm_bytes"] = L["read_bytes"] + L["write_bytes"]
     # SQ counter passes (MFMA, VALU, LDS, waits), averaged per kernel name.
     sq = {}
+    # Effective shader clock of each dispatch of the counter passes:
+    # GRBM_GUI_ACTIVE (GPU busy cycles, summed over the 8 XCDs) over the
+    # dispatch's own start / end timestamps (ns).
+    clock = {}
     for sub in ("p1", "p2"):
         for r in rows(sub, "*counter_collection.csv"):
             if engine(r["Kernel_Name"]):
-                sq.setdefault(short(r["Kernel_Name"]), {}).setdefault(
-                    r["Counter_Name"], []).append(float(r["Counter_Value"]))
+                k = short(r["Kernel_Name"])
+                sq.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(
+                    float(r["Counter_Value"]))
+                if r["Counter_Name"] == "GRBM_GUI_ACTIVE" and r.get("End_Timestamp"):
+                    ns = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                    if ns > 0:
+                        clock.setdefault(k, []).append((ns / 1000.0,
+                                                        float(r["Counter_Value"]) / 8 / ns * 1000.0))
     summary = {"launches": launches, "fetch_scale": fscale, "write_scale": wscale,
                "frames": frames}
     if args.profile_json:
@@ -503,6 +513,19 @@ def summarize_profile(args) -> int:
     print(f"\nframe: {sum(L['trace_mean_us'] for L in launches):.1f} us of kernels "
           f"({per} launches, mean over {frames - args.skip_frames} frames); "
           f"FETCH scale {fscale:.4f}, WRITE scale {wscale:.4f} (plain copy calibration)")
+    if clock:
+        print("\n| kernel | dispatch us (counter passes) | shader clock MHz (GRBM_GUI_ACTIVE / 8 / duration) |")
+        print("|---|---|---|")
+        for k in dict.fromkeys(L["kernel"] for L in launches):
+            if k in clock:
+                print(f"| `{k}` | {statistics.mean(d for d, _ in clock[k]):.1f} | "
+                      f"{statistics.mean(m for _, m in clock[k]):.0f} |")
+        summary["clock_mhz"] = {k: round(statistics.mean(m for _, m in v)) for k, v in clock.items()}
+        if args.profile_json:
+            f = Path(args.profile_json)
+            data = json.loads(f.read_text())
+            data[args.profile_key] = summary
+            f.write_text(json.dumps(data, indent=1) + "\n")
     if sq:
         def av(k, c):
             v = sq[k].get(c)
