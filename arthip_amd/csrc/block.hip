@@ -8,6 +8,7 @@
 
 #include "conv_args.h"
 #include "launch.h"
+#include "pack.h"
 #include "wino_dev.h"
 
 namespace arthip {
@@ -19,59 +20,66 @@ namespace arthip {
 //   t   = act1(conv1(in) + bias1)             (fp16, never written to HBM)
 //   out = act2(conv2(t) + bias2) + skip0 + skip1
 //
-// One 512-thread workgroup per CU walks down an output strip of 30 pixels
-// (15 Winograd tiles). Waves 0-3 (conv1) hold U1' of 16 output channels each
-// and compute t for the 32 columns the strip's conv2 tiles read (16 tiles at
-// column offset -1), one tile row (2 t rows) per step, into a 2-slot LDS ring;
-// t outside the image is stored as zero, which is conv2's padding. Waves 4-7
-// (conv2) hold U2', transform t from the ring (keeping the previous two rows in
-// registers), fold 16 tiles of which the first 15 are the strip's outputs and
-// stage them. The staged rows go to HBM a step later with the residual inputs
-// added (loaded one step ahead; the block input rows were read by conv1 a few
-// steps before and are usually still cached): stored by the conv1 waves, or
-// with two residual inputs one row of each pair by each group.
+// Both convs run Winograd F(2,3) along x and the three kernel rows directly
+// along y: for an output row y and a tile of two pixels (2t, 2t + 1),
+//   M_p = sum_dy sum_c U_dy[p][m][c] V_{y-1+dy}[p][c][t]    (p = 0..3)
+//   out(y, 2t) = M_0 + M_1 + M_2,  out(y, 2t + 1) = M_1 - M_2 - M_3
+// with V_r[p] = B^T d the 1-D transform of input row r (pixels 2t-1 .. 2t+2)
+// and U_dy = G g_dy that of kernel row dy (block_u_halfs). The MFMA sums over
+// dy and the channels, so a tile row needs 48 MFMAs per 16 output channels
+// (against 32 for F(2x2,3x3)) but each transformed input row serves the three
+// output rows that read it, the input transform is 8 packed ops per row and
+// channel quad, and U' of one conv takes 96 VGPRs per wave instead of 128.
 //
-// Both halves are winograd_strip's arithmetic: the same V' transform, fold
-// order and fp16 roundings. conv1's tiles sit at odd offsets (t columns
-// 30 s - 1 + 2 k, t rows 2 i - 1 and 2 i), where a separate launch tiles at
-// even ones; F(2x2,3x3) rounds a tile's two outputs differently, so t, and the
-// block output, agree with two separate launches to fp16 rounding rather than
-// bit for bit. The offsets are fixed relative to the image, so results do not
-// depend on the strip or workgroup that computes them. HBM traffic per block is
-// the input once (plus the 2-column halo of each strip, mostly cache hits), the
-// residual inputs and the output.
+// One 512-thread workgroup per CU (8 waves, two per SIMD, all of its LDS but
+// 32 KB) walks down an output strip of 30 pixels (15 tiles). Waves 0-3
+// (conv1) hold U1' of 16 output channels each and compute t for the 32 columns
+// the strip's conv2 tiles read (16 tiles at column offset -1), one t tile row
+// (2 t rows) per phase, into a 2-slot LDS ring; t outside the image is stored
+// as zero, which is conv2's padding. Waves 4-7 (conv2) hold U2', transform the
+// t rows from the ring, fold 16 tiles of which the first 15 are the strip's
+// outputs and stage them. The conv1 waves store the staged rows a phase later
+// with the residual inputs added.
 //
-// Per run (one strip, output tile rows j0 .. j0+len-1; t tile row i covers t
-// rows 2(j0+i)-1 and 2(j0+i), i = 0 .. len), phase k (k = 0 .. len+4) ends with
-// the workgroup barrier:
+// Transformed rows live in two 3-slot LDS rings (V1 for conv1's input, V2 for
+// t), a slot holding one row pair (4 positions x 16 tiles x 64 channels per
+// row). A fold of output tile row i reads row pairs i and i + 1 (rows 2i - 1
+// .. 2i + 2); each fragment read serves both output rows that use it.
+//
+// conv1's tiles sit at odd column offsets (t columns 30 s - 1 + 2 k), where a
+// separate launch tiles at even ones, so t, and the block output, agree with
+// two separate launches to fp16 rounding rather than bit for bit. The offsets
+// are fixed relative to the image, so results do not depend on the strip or
+// workgroup that computes them. HBM traffic per block is the input once (plus
+// the 2-column halo of each strip, mostly cache hits), the residual inputs and
+// the output.
+//
+// Per run (one strip, output tile rows j0 .. j0+len-1; input row pair Q_i =
+// padded rows 2(j0+i)-1, 2(j0+i); t tile row i covers t rows 2(j0+i)-1 and
+// 2(j0+i), i = 0 .. len), after a prologue that transforms Q_0 into V1 slot
+// 0, phase k (k = 0 .. len+4) ends with the workgroup barrier:
 //   conv1 waves: store output row k-5 from staging[(k-5)&1] with its
-//                residuals (k >= 5) and load the residuals of row k-4 (after
-//                the fold in the ReLU / no-activation block with one residual
-//                input; with two, only the first row of each pair, and the
-//                conv2 waves store and load the second);
-//                transform t_k into V1'[k&1] (k <= len) and load the input
-//                rows of t_{k+1}; fold t_{k-1} from V1'[(k-1)&1] into ring
-//                slot (k-1)&1 (1 <= k <= len+1)
+//                residuals (k >= 5) and load the residuals of row k-4;
+//                transform Q_{k+1} into V1 slot (k+1)%3 (k <= len) and load
+//                the input rows of Q_{k+2}; fold t_{k-1} from V1 slots
+//                (k-1)%3, k%3 into ring slot (k-1)&1 (1 <= k <= len+1)
 //   conv2 waves: read t_{k-2} from ring slot k&1 (2 <= k <= len+2); fold
-//                output row k-4 from V2'[k&1] into staging[k&1]
-//                (4 <= k <= len+3); with two residual inputs store the second
-//                row of output row pair k-5 and load the residuals of row k-4;
-//                transform output row k-3 into V2'[(k-3)&1] (3 <= k <= len+2)
-// Every buffer's writer and readers are a barrier apart. The store sits with
-// the conv1 waves where it can: with the conv2 waves it made theirs the
-// longer chain by about a third of a phase (timestamps per section), and
-// moved over it took the 1080p one-residual launch from 240 to 226 us.
-// With two residual inputs it is split between the two wave groups.
+//                output row k-4 from V2 slots (k-1)%3, k%3 (rows of t_{k-4},
+//                t_{k-3}) into staging[k&1] (4 <= k <= len+3); transform
+//                t_{k-2} into V2 slot (k+1)%3 (2 <= k <= len+2)
+// Every buffer's writer and readers are a barrier apart.
 struct BlockL {
   static constexpr int C = 64;
   static constexpr int PX = 2 * C;                // bytes per pixel
   static constexpr int OTILES = 15;               // output tiles per strip
   static constexpr int OPX = 2 * OTILES;          // output pixels per strip
-  static constexpr int WPS = StripLds<2>::WPS;    // halfs per V' position
-  static constexpr int VBUF = StripLds<2>::VBUF;  // halfs per V' buffer
+  static constexpr int WPS = StripLds<2>::WPS;    // halfs per position (16 tiles)
+  static constexpr int RROW = 4 * WPS;            // halfs per transformed row
+  static constexpr int RPAIR = 2 * RROW;          // halfs per ring slot (row pair)
+  static constexpr int NSLOT = 3;
   static constexpr int SBUF = StripStage<2>::SBUF;
-  static constexpr int RSLOT = 2 * 32 * C;        // halfs per ring slot (2 t rows x 32 px)
-  // Ring: pixel pairs m = x >> 1 take 256 bytes, the two pixels' halves
+  static constexpr int RSLOT = 2 * 32 * C;        // halfs per t ring slot (2 t rows x 32 px)
+  // t ring: pixel pairs m = x >> 1 take 256 bytes, the two pixels' halves
   // swapped on odd m, and the 8-byte channel quads of the pair XORed with m.
   // The conv1 folds' writes (16 tiles, one pixel and quad each) and the conv2
   // reads (2 tiles x 16 quads per 32 lanes) then both hit distinct banks.
@@ -79,76 +87,98 @@ struct BlockL {
     return row * 32 * C + (x >> 1) * 128 + (((x & 1) ^ ((x >> 1) & 1)) << 6) +
            ((q ^ ((x >> 1) & 15)) << 2);
   }
+  // Offset (halfs) of the row filters in a 64 -> 64 conv's packed weights:
+  // after U' (4 channel blocks x 16 positions x 2 chunks x 64 lanes x 8).
+  static constexpr int UOFF = 4 * 16 * 2 * 64 * 8;
   static constexpr int V1 = 0;
-  static constexpr int V2 = 2 * VBUF;
-  static constexpr int RING = 4 * VBUF;
+  static constexpr int V2 = NSLOT * RPAIR;
+  static constexpr int RING = 2 * NSLOT * RPAIR;
   static constexpr int STG = RING + 2 * RSLOT;
   static constexpr size_t lds_bytes() { return (size_t)(STG + 2 * SBUF) * 2; }
 };
 
-// Fold of 16 tiles x 16 output channels (one wave) from V' at vr[kc] + boff:
-// the four outputs of each tile, bias already in, fp32.
-__device__ __forceinline__ void block_fold(const h8 (&u)[16][2], const _Float16* const (&vr)[2],
-                                           int boff, f4 bias4, f4& y00, f4& y01, f4& y10,
-                                           f4& y11) {
+// 1-D transform of rows r = 0, 1 of a task's row pair (element 2 (4 r + j) + e
+// of x: column j, channel pair e) into positions p of a transformed row:
+// V0 = d0 - d2, V1 = d1 + d2, V2 = d2 - d1, V3 = d3 - d1 (the last negated
+// against B^T; the fold's chain absorbs it).
+__device__ __forceinline__ void row_pair_transform(_Float16* vw, const h2 (&x)[16]) {
   constexpr int WPS = BlockL::WPS;
-  auto mm = [&](int p, f4 acc) {
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          u[p][kc], *reinterpret_cast<const h8*>(vr[kc] + boff + p * WPS), acc, 0, 0, 0);
-    return acc;
-  };
-  // LLVM's single-wave small-GEMM interleave (LDS reads between the MFMAs):
-  // one-residual block 231 -> 228 us at 1080p, the SiLU block 271 -> 264 us;
-  // preset 0 measured 247 us.
-  __builtin_amdgcn_iglp_opt(1);
-  const f4 z = {0, 0, 0, 0};
-  const f4 m2 = {-2.0f, -2.0f, -2.0f, -2.0f};
+  for (int r = 0; r < 2; ++r) {
+    h2 o[4][2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    f4 P, Q;
-    if (r == 1) {
-      const f4 Y = mm(5, bias4);
-      const f4 b = mm(6, Y);
-      P = mm(4, b);
-      const f4 c = mm(7, Y);
-      Q = (c - b) + Y;
-    } else {
-      const f4 X = mm(4 * r + 2, z);
-      const f4 b = mm(4 * r + 1, X);
-      P = mm(4 * r, b);
-      const f4 c = mm(4 * r + 3, b);
-      Q = __builtin_elementwise_fma(X, m2, c);
+    for (int e = 0; e < 2; ++e) {
+      const h2 d0 = x[2 * (4 * r) + e], d1 = x[2 * (4 * r + 1) + e];
+      const h2 d2 = x[2 * (4 * r + 2) + e], d3 = x[2 * (4 * r + 3) + e];
+      o[0][e] = pk_sub(d0, d2);
+      o[1][e] = d1 + d2;
+      o[2][e] = pk_sub(d2, d1);
+      o[3][e] = pk_sub(d3, d1);
     }
-    if (r == 0) {
-      y00 = P;
-      y01 = Q;
-    } else if (r == 1) {
-      y00 += P;
-      y01 += Q;
-      y10 = P;
-      y11 = Q;
-    } else if (r == 2) {
-      y00 += P;
-      y01 += Q;
-      y10 -= P;
-      y11 -= Q;
-    } else {
-      y10 -= P;
-      y11 -= Q;
-    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      *reinterpret_cast<h4*>(vw + r * BlockL::RROW + p * WPS) =
+          __builtin_shufflevector(o[p][0], o[p][1], 0, 1, 2, 3);
   }
 }
 
-// Phases k = 0 .. len + 4 of one run, two per iteration so that the buffer
-// parity is a compile-time constant: ph(parity_tag, k).
+// Fold of one tile row (two output rows) x 16 output channels (one wave) from
+// transformed row pairs A (rows R0, R1) and B (R2, R3) at vr[kc] + offA / offB:
+// output row 0 reads R0..R2 (dy = 0..2), row 1 R1..R3. Chains per output row
+// (the accumulator carries them): X = M2, b = X + bias + M1, P = b + M0 and
+// c = b + M3' (M3' = -M3 from the negated V3); y0 = P, y1 = c - 2 X.
+__device__ __forceinline__ void block_fold(const h8 (&u)[3][4][2], const _Float16* const (&vr)[2],
+                                           int offA, int offB, f4 bias4, f4& y00, f4& y01,
+                                           f4& y10, f4& y11) {
+  constexpr int WPS = BlockL::WPS;
+  constexpr int RROW = BlockL::RROW;
+  auto pos = [&](int p, f4& a0, f4& a1) {
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const h8 f0 = *reinterpret_cast<const h8*>(vr[kc] + offA + p * WPS);
+      const h8 f1 = *reinterpret_cast<const h8*>(vr[kc] + offA + RROW + p * WPS);
+      const h8 f2 = *reinterpret_cast<const h8*>(vr[kc] + offB + p * WPS);
+      const h8 f3 = *reinterpret_cast<const h8*>(vr[kc] + offB + RROW + p * WPS);
+      a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[0][p][kc], f0, a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[0][p][kc], f1, a1, 0, 0, 0);
+      a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[1][p][kc], f1, a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[1][p][kc], f2, a1, 0, 0, 0);
+      a0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[2][p][kc], f2, a0, 0, 0, 0);
+      a1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[2][p][kc], f3, a1, 0, 0, 0);
+    }
+  };
+  __builtin_amdgcn_iglp_opt(1);
+  const f4 m2 = {-2.0f, -2.0f, -2.0f, -2.0f};
+  f4 X0 = {0, 0, 0, 0}, X1 = {0, 0, 0, 0};
+  pos(2, X0, X1);
+  f4 b0 = X0 + bias4, b1 = X1 + bias4;
+  pos(1, b0, b1);
+  f4 c0 = b0, c1 = b1;
+  pos(0, b0, b1);
+  pos(3, c0, c1);
+  y00 = b0;
+  y10 = b1;
+  y01 = __builtin_elementwise_fma(X0, m2, c0);
+  y11 = __builtin_elementwise_fma(X1, m2, c1);
+}
+
+// Phases k = 0 .. len + 4 of one run, six per iteration so that k % 6, and
+// with it the t ring and staging parity and the three row-pair slots, is a
+// compile-time constant (every LDS offset an immediate): ph(k6_tag, k).
 template <class F>
 __device__ __forceinline__ void block_phases(int len, F&& ph) {
   for (int k = 0;;) {
     ph(IntC<0>{}, k);
     if (++k > len + 4) break;
     ph(IntC<1>{}, k);
+    if (++k > len + 4) break;
+    ph(IntC<2>{}, k);
+    if (++k > len + 4) break;
+    ph(IntC<3>{}, k);
+    if (++k > len + 4) break;
+    ph(IntC<4>{}, k);
+    if (++k > len + 4) break;
+    ph(IntC<5>{}, k);
     if (++k > len + 4) break;
   }
 }
@@ -159,9 +189,8 @@ winograd_block(BlockArgs a) {
   using L = BlockL;
   constexpr int C = L::C;
   constexpr int PX = L::PX;
-  constexpr int WPS = L::WPS;
-  constexpr int VBUF = L::VBUF;
   constexpr int SBUF = L::SBUF;
+  constexpr int RPAIR = L::RPAIR;
   constexpr uint32_t kOob = 0x80000000u;
   extern __shared__ __attribute__((aligned(16))) _Float16 blds[];
   const int tid = threadIdx.x;
@@ -194,28 +223,15 @@ winograd_block(BlockArgs a) {
   const int gtid = tid & 255;
   const int tt = gtid >> 4;
   const int tq = gtid & 15;
+  // Row pair slots of phase k (from k6 = k % 6): the fold reads (k-1)%3 and
+  // k%3, the transform writes (k+1)%3.
 
-  // Store phase: thread handles 16-byte group sg of pixel sx in a row of the
-  // output row pair that left the conv2 fold last phase. With up to one
-  // residual input the conv1 waves store both rows (1080p, one residual:
-  // 240 us with the conv2 waves storing, 226 with conv1; split, 229). With
-  // two, holding both rows' residual registers across the conv1 fold costs
-  // more than it saves (280 against 260 us), so the rows are split: the conv1
-  // waves store row 0 and the conv2 waves row 1, each holding one row's
-  // residuals (259 -> 241 us).
-  constexpr int kConv1Rows = NSKIP < 2 ? 2 : 1;  // rows [0, kConv1Rows) in conv1
+  // Store phase (conv1 waves): thread handles 16-byte group sg of pixel sx in
+  // both rows of the output row pair that left the conv2 fold last phase.
   // The conv1 waves load the next row's residuals right after the store, or,
   // in the ReLU / no-activation block with one residual input, after their
-  // fold, so that those registers are not live across it: that block 227.0
-  // -> 224.6 us at 1080p, while the same order took the SiLU block from 265 to
-  // 284-293 us and the two-residual block from 240 to 260 us.
+  // fold, so that those registers are not live across it.
   constexpr bool kSkipsAfterFold = ACT1 != kActSilu && NSKIP == 1;
-  // With act1 ReLU or none, conv1 runs on U1' / 4 and bias1 / 4 and the ring
-  // holds t / 4: the power-of-two scale commutes with the activation and with
-  // every fp16 and fp32 rounding (outside the subnormal range), so conv2's
-  // transform of the ring equals the 1/4-scaled transform of t and drops its
-  // own 1/4 (16 of 64 packed ops per transform). SiLU does not commute.
-  constexpr bool kQuarterT = ACT1 != kActSilu;
   _Float16* const stg = blds + L::STG;
   const int sx = gtid >> 3;
   const int sg = gtid & 7;
@@ -239,8 +255,7 @@ winograd_block(BlockArgs a) {
     const bool ok = live && (r == 0 || 2 * o + 1 < a.H);  // uniform
     return ok ? lane_off + (uint32_t)r * rb32 : kOob;
   };
-  // Rows [ra, rb) of the pair.
-  auto load_skips = [&](bool live, int o, int ra, int rb) {
+  auto load_skips = [&](bool live, int o) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
@@ -249,15 +264,15 @@ winograd_block(BlockArgs a) {
     for (int k = 0; k < NSKIP; ++k) {
       const __amdgpu_buffer_rsrc_t rs = row_rsrc(k == 0 ? a.skip0 : a.skip1, o);
 #pragma unroll
-      for (int r = ra; r < rb; ++r)
+      for (int r = 0; r < 2; ++r)
         skr[k][r] = __builtin_bit_cast(
             h8, __builtin_amdgcn_raw_buffer_load_b128(rs, st_off(live, o, r), 0, kNonTemporal));
     }
   };
-  auto store_row = [&](bool live, int o, int SB, int ra, int rb) {
+  auto store_row = [&](bool live, int o, int SB) {
     const __amdgpu_buffer_rsrc_t rs = row_rsrc(a.out, o);
 #pragma unroll
-    for (int r = ra; r < rb; ++r) {
+    for (int r = 0; r < 2; ++r) {
       h8 v = act8<ACT2>(*reinterpret_cast<const h8*>(stg + SB * SBUF + sr0 + r * 32 * C));
       if (NSKIP > 0) v += skr[0][r];
       if (NSKIP > 1) v += skr[1][r];
@@ -265,24 +280,22 @@ winograd_block(BlockArgs a) {
                                              kCachedOut ? 0 : kNonTemporal);
     }
   };
+  // U' of this wave: [dy][position][kc], 16 output channels.
+  auto load_u = [&](const uint16_t* packed, h8 (&u)[3][4][2]) {
+    const h8* up = reinterpret_cast<const h8*>(packed + L::UOFF) +
+                   (size_t)grp * (12 * 2 * 64) + lane;
+#pragma unroll
+    for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) u[dy][p][kc] = up[((dy * 4 + p) * 2 + kc) * 64];
+  };
   if (wave < 4) {
     // ---------------- conv1: in -> t ----------------------------------------
-    h8 u[16][2];
-    {
-      const h8* up = reinterpret_cast<const h8*>(a.u1) + (size_t)grp * (16 * 2 * 64) + lane;
-#pragma unroll
-      for (int p = 0; p < 16; ++p)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) u[p][kc] = up[(p * 2 + kc) * 64];
-    }
-    f4 bias4 = *reinterpret_cast<const f4*>(a.bias1 + ch0);
-    if constexpr (kQuarterT) {
-#pragma unroll
-      for (int p = 0; p < 16; ++p)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) u[p][kc] *= (_Float16)0.25f;
-      bias4 *= 0.25f;
-    }
+    h8 u[3][4][2];
+    load_u(a.u1, u);
+    const f4 bias4 = *reinterpret_cast<const f4*>(a.bias1 + ch0);
     _Float16* const vw = blds + L::V1 + StripLds<2>::at(tt, 4 * tq);
     const _Float16* vr[2];
 #pragma unroll
@@ -325,29 +338,25 @@ winograd_block(BlockArgs a) {
     };
     // Lane masks (all ones or zero) of this lane's two t columns, per run.
     uint32_t cm0 = 0, cm1 = 0;
-    h2 A[16], B[16];
-    auto phase = [&](auto par_tag, int k, int len) {
-      constexpr int P = decltype(par_tag)::value;  // k & 1
-      h2(&top)[16] = P ? B : A;
-      h2(&bot)[16] = P ? A : B;
+    h2 X[16];  // input rows of the next row pair to transform
+    auto phase = [&](auto k6_tag, int k, int len) {
+      constexpr int K6 = decltype(k6_tag)::value;  // k % 6
+      constexpr int P = K6 & 1;
+      constexpr int SA = ((K6 + 2) % 3) * RPAIR, SB = (K6 % 3) * RPAIR, SW = ((K6 + 1) % 3) * RPAIR;
       // Output row k-5 leaves staging (k-5)&1 = P^1 (the conv2 fold of the
       // last phase); its residuals were loaded last phase. Then the residuals
       // of row k-4 (folded by conv2 this phase, stored next phase).
-      store_row(k >= 5, j0 + k - 5, P ^ 1, 0, kConv1Rows);
-      if constexpr (!kSkipsAfterFold)
-        load_skips(k >= 4 && k <= len + 3, j0 + k - 4, 0, kConv1Rows);
-      // Transform first, fold second: the conv2 wave on the same SIMD folds
-      // first, so one wave's VALU transform overlaps the other's MFMA chain
-      // (and the next input rows are requested earlier).
+      store_row(k >= 5, j0 + k - 5, P ^ 1);
+      if constexpr (!kSkipsAfterFold) load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
       if (k <= len) {
-        v_transform<WPS>(vw + P * VBUF, top, bot);
-        // t_{k+1} needs padded input rows 2 (j0 + k + 1) + 1 and + 2.
-        load2(top, 2 * (j0 + k) + 3);
+        row_pair_transform(vw + SW, X);
+        // Q_{k+2}: padded rows 2 (j0 + k + 2) - 1 and 2 (j0 + k + 2).
+        load2(X, 2 * (j0 + k) + 3);
       }
       if (k >= 1 && k <= len + 1) {
-        // Fold t_{k-1}: t rows 2 (j0 + k - 1) - 1 + dy, t columns 30 s - 1 + 2 tcol + dx.
+        // Fold t_{k-1}: t rows 2 (j0 + k - 1) - 1 + r, t columns 30 s - 1 + 2 tcol + dx.
         f4 y00, y01, y10, y11;
-        block_fold(u, vr, (P ^ 1) * VBUF, bias4, y00, y01, y10, y11);
+        block_fold(u, vr, SA, SB, bias4, y00, y01, y10, y11);
         const int tr0 = 2 * (j0 + k - 1) - 1;
         const uint32_t rm0 = (tr0 >= 0 && tr0 < a.H) ? ~0u : 0u;  // uniform
         const uint32_t rm1 = (tr0 + 1 < a.H) ? ~0u : 0u;
@@ -364,8 +373,7 @@ winograd_block(BlockArgs a) {
         *reinterpret_cast<u2*>(sl + rw[2]) = masked(y10, rm1 & cm0);
         *reinterpret_cast<u2*>(sl + rw[3]) = masked(y11, rm1 & cm1);
       }
-      if constexpr (kSkipsAfterFold)
-        load_skips(k >= 4 && k <= len + 3, j0 + k - 4, 0, kConv1Rows);
+      if constexpr (kSkipsAfterFold) load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
       lds_sync();
     };
     for (int it = begin; it < end;) {
@@ -387,9 +395,12 @@ winograd_block(BlockArgs a) {
         run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
         lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
       }
-      // t_0 needs padded rows 2 j0 - 1 .. 2 j0 + 2.
-      load2(A, 2 * j0 - 1);
-      load2(B, 2 * j0 + 1);
+      // Prologue: Q_0 (padded rows 2 j0 - 1, 2 j0) into V1 slot 0, then the
+      // rows of Q_1 for phase 0. Slot 0 is free: the last fold of an earlier
+      // run read it at least three barriers ago.
+      load2(X, 2 * j0 - 1);
+      row_pair_transform(vw, X);
+      load2(X, 2 * j0 + 1);
       block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
       it += len;
     }
@@ -397,14 +408,8 @@ winograd_block(BlockArgs a) {
   }
 
   // ---------------- conv2: t -> out ------------------------------------------
-  h8 u[16][2];
-  {
-    const h8* up = reinterpret_cast<const h8*>(a.u2) + (size_t)grp * (16 * 2 * 64) + lane;
-#pragma unroll
-    for (int p = 0; p < 16; ++p)
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) u[p][kc] = up[(p * 2 + kc) * 64];
-  }
+  h8 u[3][4][2];
+  load_u(a.u2, u);
   const f4 bias4 = *reinterpret_cast<const f4*>(a.bias2 + ch0);
   _Float16* const vw = blds + L::V2 + StripLds<2>::at(tt, 4 * tq);
   const _Float16* vr[2];
@@ -432,38 +437,26 @@ winograd_block(BlockArgs a) {
       }
   };
   const int sw0 = StripStage<2>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
-  h2 A[16], B[16];
-  auto phase = [&](auto par_tag, int k, int len) {
-    constexpr int P = decltype(par_tag)::value;  // k & 1
-    h2(&cur)[16] = P ? B : A;
-    h2(&nxt)[16] = P ? A : B;
-    // t_{k-2} from ring slot k&1 into `nxt`; with t_{k-3} in `cur` that is the
-    // patch of output row k-3. Read at the start of the phase, so that these
-    // LDS reads overlap the fold (the registers they land in are live all phase
-    // anyway): one-residual block 222.0 -> 219.8 us, SiLU block 260 -> 255 us,
-    // two-residual block (its store after the fold) 230.9 -> 228.6 us.
-    if (k >= 2 && k <= len + 2) ring_load2(nxt, P);
+  h2 T[16];
+  auto phase = [&](auto k6_tag, int k, int len) {
+    constexpr int K6 = decltype(k6_tag)::value;  // k % 6
+    constexpr int P = K6 & 1;
+    constexpr int SA = ((K6 + 2) % 3) * RPAIR, SB = (K6 % 3) * RPAIR, SW = ((K6 + 1) % 3) * RPAIR;
+    // t_{k-2} from ring slot k&1, read at the start of the phase so that
+    // these LDS reads overlap the fold.
+    const bool tr = k >= 2 && k <= len + 2;
+    if (tr) ring_load2(T, P);
     const bool fold = k >= 4 && k <= len + 3;
     if (fold) {
       f4 y00, y01, y10, y11;
-      block_fold(u, vr, P * VBUF, bias4, y00, y01, y10, y11);
+      block_fold(u, vr, SA, SB, bias4, y00, y01, y10, y11);
       _Float16* sw = stg + P * SBUF + sw0;
       *reinterpret_cast<h4*>(sw) = strip_act4<kActNone>(y00);
       *reinterpret_cast<h4*>(sw + C) = strip_act4<kActNone>(y01);
       *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<kActNone>(y10);
       *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<kActNone>(y11);
     }
-    // With two residual inputs: output row k-5 leaves staging (k-5)&1 = P^1
-    // with the residuals loaded last phase (after the fold: 243 -> 235 us
-    // against before it), then the residuals of the row just folded (stored
-    // next phase), issued after the fold so that they are not live across it.
-    if constexpr (kConv1Rows < 2) {
-      store_row(k >= 5, j0 + k - 5, P ^ 1, kConv1Rows, 2);
-      load_skips(fold, j0 + k - 4, kConv1Rows, 2);
-    }
-    if (k >= 2 && k <= len + 2) {
-      if (k >= 3) v_transform<WPS, !kQuarterT>(vw + (P ^ 1) * VBUF, cur, nxt);
-    }
+    if (tr) row_pair_transform(vw + SW, T);
     lds_sync();
   };
   for (int it = begin; it < end;) {
@@ -508,6 +501,9 @@ bool block_eligible(int C, int M, int act1, int act2, int64_t N, int64_t H, int6
 
 hipError_t launch_block(BlockArgs a, hipStream_t s) {
   if (!block_eligible(64, 64, a.act1, a.act2, a.N, a.H, a.W)) return hipErrorInvalidValue;
+  // The kernel finds the row filters at a fixed offset of the packed weights.
+  if (block_u_offset(64, 64) != (size_t)BlockL::UOFF || block_u_halfs(64, 64) == 0)
+    return hipErrorInvalidValue;
   if (a.skip0 == nullptr && a.skip1 != nullptr) {
     a.skip0 = a.skip1;
     a.skip1 = nullptr;

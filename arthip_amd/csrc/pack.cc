@@ -20,8 +20,14 @@ size_t winograd_u_halfs(int C, int M) {
   return static_cast<size_t>(g.n_ob) * 16 * g.kc * 64 * 8;
 }
 
+size_t block_u_halfs(int C, int M) {
+  return (C == 64 && M == 64) ? static_cast<size_t>(M / 16) * 12 * (C / 32) * 64 * 8 : 0;
+}
+
+size_t block_u_offset(int C, int M) { return winograd_u_halfs(C, M) + narrow_packed_halfs(C, M); }
+
 size_t winograd_packed_halfs(int C, int M) {
-  return winograd_u_halfs(C, M) + narrow_packed_halfs(C, M);
+  return winograd_u_halfs(C, M) + narrow_packed_halfs(C, M) + block_u_halfs(C, M);
 }
 
 void winograd_pack(const float* w, int M, int C, uint16_t* out) {
@@ -45,6 +51,26 @@ void winograd_pack(const float* w, int M, int C, uint16_t* out) {
   // G = [[1,0,0],[1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]]; U = G g G^T in double,
   // scaled by 4 (exact), rounded once to fp16.
   static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+  if (block_u_halfs(C, M) != 0) {
+    // Row filters of the fused block: U_dy[p] = G[p] . w[dy][0..2], rounded once.
+    uint16_t* bu = out + block_u_offset(C, M);
+    const int kcn = C / 32;
+    for (int m = 0; m < M; ++m) {
+      const int ob = m / 16, row = m % 16;
+      for (int c = 0; c < C; ++c) {
+        const float* k = w + (static_cast<size_t>(m) * C + c) * 9;
+        const int kc = c / 32, kk = c % 32;
+        const int lane = row + 16 * (kk / 8), e = kk % 8;
+        for (int dy = 0; dy < 3; ++dy)
+          for (int p = 0; p < 4; ++p) {
+            const double u = G[p][0] * k[dy * 3] + G[p][1] * k[dy * 3 + 1] + G[p][2] * k[dy * 3 + 2];
+            const size_t idx =
+                ((((static_cast<size_t>(ob) * 3 + dy) * 4 + p) * kcn + kc) * 64 + lane) * 8 + e;
+            bu[idx] = f32_to_f16(static_cast<float>(u));
+          }
+      }
+    }
+  }
   for (int m = 0; m < M; ++m) {
     const int ob = m / 16, row = m % 16;
     for (int c = 0; c < C; ++c) {

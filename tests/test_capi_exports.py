@@ -71,7 +71,10 @@ def test_winograd_pack_layout():
         assert rc == 0
         kc = (c_in + 31) // 32
         n_ob = (m_out + 15) // 16
-        up = u.view(np.float16).reshape(n_ob, 16, kc, 64, 8).astype(np.float64)
+        n_wino = n_ob * 16 * kc * 64 * 8
+        # 64 -> 64 also carries the fused block's row filters after U'.
+        assert n_u == n_wino + (n_ob * 12 * kc * 64 * 8 if (c_in, m_out) == (64, 64) else 0)
+        up = u[:n_wino].view(np.float16).reshape(n_ob, 16, kc, 64, 8).astype(np.float64)
         for m in range(m_out):
             for c in range(c_in):
                 want = (4.0 * orc.winograd_filter(w[m, c].astype(np.float64))).astype(np.float16)
@@ -89,6 +92,88 @@ def test_winograd_pack_layout():
         assert not up[mask].any()
         np.testing.assert_array_equal(b[:m_out], bias.astype(np.float32))
         assert not b[m_out:].any()
+
+
+G_ROW = np.array([[1, 0, 0], [0.5, 0.5, 0.5], [0.5, -0.5, 0.5], [0, 0, 1]])
+
+
+def _packed_64(w):
+    lib = _lib.lib()
+    n_u = lib.arthip_conv3x3_packed_halfs(64, 64)
+    u = np.zeros(n_u, np.uint16)
+    b = np.zeros(lib.arthip_conv3x3_bias_len(64), np.float32)
+    rc = lib.arthip_conv3x3_pack(
+        w.view(np.uint16).ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), None, 64, 64,
+        u.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n_u,
+        b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), b.size)
+    assert rc == 0
+    return u[4 * 16 * 2 * 64 * 8:].view(np.float16).reshape(4, 3, 4, 2, 64, 8).astype(np.float64)
+
+
+def test_block_row_filter_layout():
+    """The fused block's row filters after U' of a 64 -> 64 conv:
+    [ob][dy][p][kc][lane][e] = fp16(G[p] . w[m][c][dy][:]) with m = 16*ob + lane % 16 and
+    c = 32*kc + 8*(lane // 16) + e."""
+    w = (np.random.default_rng(8).standard_normal((64, 64, 3, 3)) * 0.2).astype(np.float16)
+    up = _packed_64(w)
+    want = np.einsum("pj,mcyj->mcyp", G_ROW, w.astype(np.float64)).astype(np.float16)
+    m = np.arange(64)[:, None]
+    c = np.arange(64)[None, :]
+    ob, row = m // 16, m % 16
+    kc, kk = c // 32, c % 32
+    lane, e = row + 16 * (kk // 8), kk % 8
+    for dy in range(3):
+        for p in range(4):
+            got = up[ob, dy, p, kc, lane, e]
+            np.testing.assert_array_equal(got, want[:, :, dy, p].astype(np.float64))
+
+
+def test_block_row_winograd_reproduces_the_conv():
+    """The fused block's arithmetic on the CPU, from the packed row filters: per
+    transformed input row V = (d0 - d2, d1 + d2, d2 - d1, d3 - d1) (the last
+    negated), M_p = sum over kernel rows and channels of U_dy[p] V_dy[p], and the
+    fold's chains X = M2, b = X + M1, P = b + M0, c = b + M3, outputs P and
+    c - 2 X, equal the two outputs of a direct 3x3 correlation (fp64, the
+    filters as packed in fp16). A planted sign error in V3 or in the fold fails."""
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((64, 64, 3, 3)) * 0.2).astype(np.float16)
+    up = _packed_64(w)
+    # U[m][c][dy][p] back from the A-operand layout.
+    u = np.zeros((64, 64, 3, 4))
+    m = np.arange(64)[:, None]
+    c = np.arange(64)[None, :]
+    lane, e = m % 16 + 16 * ((c % 32) // 8), (c % 32) % 8
+    for dy in range(3):
+        for p in range(4):
+            u[:, :, dy, p] = up[m // 16, dy, p, c // 32, lane, e]
+    d = rng.standard_normal((64, 3, 4))  # channel, kernel row, 4 pixels
+
+    def fold(v3_sign=1.0, q_coef=-2.0):
+        v = np.stack([d[..., 0] - d[..., 2], d[..., 1] + d[..., 2], d[..., 2] - d[..., 1],
+                      v3_sign * (d[..., 3] - d[..., 1])], axis=-1)  # [c][dy][p]
+        mp = np.einsum("mcyp,cyp->mp", u, v)
+        x = mp[:, 2]
+        b = x + mp[:, 1]
+        return b + mp[:, 0], b + mp[:, 3] + q_coef * x
+
+    # Direct correlation with the taps the rounded filters imply: for any U,
+    # output 0 is taps (U0, U1 - U2, U1 + U2 - U0) on pixels 0..2 and output 1
+    # taps (U1 + U2 - U3, U1 - U2, U3) on pixels 1..3 (exact identities of F(2,3)).
+    u0, u1, u2, u3 = (u[..., p] for p in range(4))
+    t0 = np.stack([u0, u1 - u2, u1 + u2 - u0], axis=-1)  # [m][c][dy][dx]
+    t1 = np.stack([u1 + u2 - u3, u1 - u2, u3], axis=-1)
+    y0 = np.einsum("mcyx,cyx->m", t0, d[..., 0:3])
+    y1 = np.einsum("mcyx,cyx->m", t1, d[..., 1:4])
+    g0, g1 = fold()
+    np.testing.assert_allclose(g0, y0, rtol=0, atol=1e-9)
+    np.testing.assert_allclose(g1, y1, rtol=0, atol=1e-9)
+    # Those taps are the model's within the fp16 rounding of U.
+    w64 = w.astype(np.float64)
+    assert np.abs(t0 - w64).max() < 4e-3 and np.abs(t1 - w64).max() < 4e-3
+    bad0, bad1 = fold(v3_sign=-1.0)
+    assert np.abs(bad1 - y1).max() > 1e-2
+    bad0, bad1 = fold(q_coef=2.0)
+    assert np.abs(bad1 - y1).max() > 1e-2
 
 
 def test_padded_dims():
