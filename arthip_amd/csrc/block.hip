@@ -31,15 +31,23 @@ namespace arthip {
 // output rows that read it, the input transform is 8 packed ops per row and
 // channel quad, and U' of one conv takes 96 VGPRs per wave instead of 128.
 //
-// One 512-thread workgroup per CU (8 waves, two per SIMD, all of its LDS but
-// 32 KB) walks down an output strip of 30 pixels (15 tiles). Waves 0-3
-// (conv1) hold U1' of 16 output channels each and compute t for the 32 columns
-// the strip's conv2 tiles read (16 tiles at column offset -1), one t tile row
-// (2 t rows) per phase, into a 2-slot LDS ring; t outside the image is stored
-// as zero, which is conv2's padding. Waves 4-7 (conv2) hold U2', transform the
-// t rows from the ring, fold 16 tiles of which the first 15 are the strip's
-// outputs and stage them. The conv1 waves store the staged rows a phase later
-// with the residual inputs added.
+// One 768-thread workgroup per CU (12 waves, three per SIMD, 128 KB of LDS)
+// walks down an output strip of 30 pixels (15 tiles), one output tile row
+// per phase. The three waves of a SIMD do different jobs, so that one wave's
+// memory and VALU work runs beside the other two waves' MFMA chains:
+//   waves 0-3  (conv1 fold) hold U1' of 16 output channels each and fold t
+//              for the 32 columns the strip's conv2 tiles read (16 tiles at
+//              column offset -1), one t tile row (2 t rows) per phase, into a
+//              2-slot LDS ring; t outside the image is stored as zero, which
+//              is conv2's padding;
+//   waves 4-7  (conv2 fold) hold U2' and fold 16 tiles of which the first 15
+//              are the strip's outputs into staging;
+//   waves 8-11 load the input rows, transform them and the t rows from the
+//              ring, and store the staged rows a phase later with the residual
+//              inputs added.
+// U' of one conv takes 96 VGPRs per wave, which leaves the fold waves room in
+// the 168 VGPRs of three waves per SIMD (F(2x2,3x3)'s 128 did not: the folds
+// spilled).
 //
 // Transformed rows live in two 3-slot LDS rings (V1 for conv1's input, V2 for
 // t), a slot holding one row pair (4 positions x 16 tiles x 64 channels per
@@ -57,16 +65,17 @@ namespace arthip {
 // Per run (one strip, output tile rows j0 .. j0+len-1; input row pair Q_i =
 // padded rows 2(j0+i)-1, 2(j0+i); t tile row i covers t rows 2(j0+i)-1 and
 // 2(j0+i), i = 0 .. len), after a prologue that transforms Q_0 into V1 slot
-// 0, phase k (k = 0 .. len+4) ends with the workgroup barrier:
-//   conv1 waves: store output row k-5 from staging[(k-5)&1] with its
-//                residuals (k >= 5) and load the residuals of row k-4;
-//                transform Q_{k+1} into V1 slot (k+1)%3 (k <= len) and load
-//                the input rows of Q_{k+2}; fold t_{k-1} from V1 slots
-//                (k-1)%3, k%3 into ring slot (k-1)&1 (1 <= k <= len+1)
-//   conv2 waves: read t_{k-2} from ring slot k&1 (2 <= k <= len+2); fold
-//                output row k-4 from V2 slots (k-1)%3, k%3 (rows of t_{k-4},
-//                t_{k-3}) into staging[k&1] (4 <= k <= len+3); transform
-//                t_{k-2} into V2 slot (k+1)%3 (2 <= k <= len+2)
+// 0 and a barrier, phase k (k = 0 .. len+4) ends with the workgroup barrier:
+//   conv1 waves:     fold t_{k-1} from V1 slots (k-1)%3, k%3 into ring slot
+//                    (k-1)&1 (1 <= k <= len+1)
+//   conv2 waves:     fold output row k-4 from V2 slots (k-1)%3, k%3 (rows of
+//                    t_{k-4}, t_{k-3}) into staging[k&1] (4 <= k <= len+3)
+//   load and store   read t_{k-2} from ring slot k&1 (2 <= k <= len+2); store
+//   waves:           output row k-5 from staging[(k-5)&1] with its residuals
+//                    (k >= 5) and load the residuals of row k-4; transform
+//                    Q_{k+1} into V1 slot (k+1)%3 (k <= len) and load the
+//                    input rows of Q_{k+2}; transform t_{k-2} into V2 slot
+//                    (k+1)%3 (2 <= k <= len+2)
 // Every buffer's writer and readers are a barrier apart.
 struct BlockL {
   static constexpr int C = 64;
@@ -77,6 +86,7 @@ struct BlockL {
   static constexpr int RROW = 4 * WPS;            // halfs per transformed row
   static constexpr int RPAIR = 2 * RROW;          // halfs per ring slot (row pair)
   static constexpr int NSLOT = 3;
+  static constexpr int THREADS = 768;             // 12 waves, three per SIMD
   static constexpr int SBUF = StripStage<2>::SBUF;
   static constexpr int RSLOT = 2 * 32 * C;        // halfs per t ring slot (2 t rows x 32 px)
   // t ring: pixel pairs m = x >> 1 take 256 bytes, the two pixels' halves
@@ -184,7 +194,7 @@ __device__ __forceinline__ void block_phases(int len, F&& ph) {
 }
 
 template <int ACT1, int ACT2, int NSKIP, bool kCachedOut>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(BlockL::THREADS) __attribute__((amdgpu_waves_per_eu(3, 3)))
 winograd_block(BlockArgs a) {
   using L = BlockL;
   constexpr int C = L::C;
@@ -213,25 +223,120 @@ winograd_block(BlockArgs a) {
     s = (int)(sgl - nn * (uint32_t)a.n_strips);
     n = (int)nn;
   };
-  // MFMA lane: tile tcol, B rows 8*kq.. of each 32-channel chunk, output
-  // channels [ch0, ch0 + 4) of the tile's four pixels.
+  // MFMA lane of the fold waves: tile tcol, B rows 8*kq.. of each 32-channel
+  // chunk, output channels [ch0, ch0 + 4) of the tile's four pixels.
   const int grp = wave & 3;  // 16-channel block within the conv
   const int tcol = lane & 15;
   const int kq = lane >> 4;
   const int ch0 = 16 * grp + 4 * kq;
-  // Transform task (both halves): tile tt, channel quad tq.
-  const int gtid = tid & 255;
+
+  if (wave < 8) {
+    // ---------------- fold waves ---------------------------------------------
+    const bool c1 = wave < 4;
+    // U' of this wave: [dy][position][kc], 16 output channels.
+    h8 u[3][4][2];
+    {
+      const h8* up = reinterpret_cast<const h8*>((c1 ? a.u1 : a.u2) + L::UOFF) +
+                     (size_t)grp * (12 * 2 * 64) + lane;
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) u[dy][p][kc] = up[((dy * 4 + p) * 2 + kc) * 64];
+    }
+    const f4 bias4 = *reinterpret_cast<const f4*>((c1 ? a.bias1 : a.bias2) + ch0);
+    const int vbase = c1 ? L::V1 : L::V2;
+    const _Float16* vr[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) vr[kc] = blds + vbase + StripLds<2>::at(tcol, 32 * kc + 8 * kq);
+    if (c1) {
+      // ---------------- conv1: V1 -> t ring ------------------------------------
+      _Float16* const ring = blds + L::RING;
+      // Ring offsets of this lane's four t values (pixel rows 0/1, columns
+      // 2 tcol / 2 tcol + 1, channel quad 4 grp + kq).
+      int rw[4];
+      {
+        const int q = 4 * grp + kq;
+        rw[0] = L::at(0, 2 * tcol, q);
+        rw[1] = L::at(0, 2 * tcol + 1, q);
+        rw[2] = L::at(1, 2 * tcol, q);
+        rw[3] = L::at(1, 2 * tcol + 1, q);
+      }
+      // Lane masks (all ones or zero) of this lane's two t columns, per run.
+      uint32_t cm0 = 0, cm1 = 0;
+      auto phase = [&](auto k6_tag, int k, int len) {
+        constexpr int K6 = decltype(k6_tag)::value;  // k % 6
+        constexpr int P = K6 & 1;
+        constexpr int SA = ((K6 + 2) % 3) * RPAIR, SB = (K6 % 3) * RPAIR;
+        if (k >= 1 && k <= len + 1) {
+          // Fold t_{k-1}: t rows 2 (j0 + k - 1) - 1 + r, t columns 30 s - 1 + 2 tcol + dx.
+          f4 y00, y01, y10, y11;
+          block_fold(u, vr, SA, SB, bias4, y00, y01, y10, y11);
+          const int tr0 = 2 * (j0 + k - 1) - 1;
+          const uint32_t rm0 = (tr0 >= 0 && tr0 < a.H) ? ~0u : 0u;  // uniform
+          const uint32_t rm1 = (tr0 + 1 < a.H) ? ~0u : 0u;
+          // t outside the image is stored as zero (bitwise, so that no branch
+          // splits the phase).
+          auto masked = [&](f4 y, uint32_t m) {
+            u2 b = __builtin_bit_cast(u2, strip_act4<ACT1>(y));
+            b &= u2{m, m};
+            return b;
+          };
+          _Float16* sl = ring + (P ^ 1) * L::RSLOT;
+          *reinterpret_cast<u2*>(sl + rw[0]) = masked(y00, rm0 & cm0);
+          *reinterpret_cast<u2*>(sl + rw[1]) = masked(y01, rm0 & cm1);
+          *reinterpret_cast<u2*>(sl + rw[2]) = masked(y10, rm1 & cm0);
+          *reinterpret_cast<u2*>(sl + rw[3]) = masked(y11, rm1 & cm1);
+        }
+        lds_sync();
+      };
+      for (int it = begin; it < end;) {
+        decode(it);
+        const int len = min(end - it, a.tiles_h - j0);
+        const int tc0 = L::OPX * s - 1 + 2 * tcol;
+        cm0 = (tc0 >= 0 && tc0 < a.W) ? ~0u : 0u;
+        cm1 = (tc0 + 1 < a.W) ? ~0u : 0u;
+        lds_sync();  // the prologue's transform of Q_0
+        block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
+        it += len;
+      }
+      return;
+    }
+    // ---------------- conv2: V2 -> staging ------------------------------------
+    _Float16* const stg = blds + L::STG;
+    const int sw0 = StripStage<2>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
+    auto phase = [&](auto k6_tag, int k, int len) {
+      constexpr int K6 = decltype(k6_tag)::value;  // k % 6
+      constexpr int P = K6 & 1;
+      constexpr int SA = ((K6 + 2) % 3) * RPAIR, SB = (K6 % 3) * RPAIR;
+      if (k >= 4 && k <= len + 3) {
+        f4 y00, y01, y10, y11;
+        block_fold(u, vr, SA, SB, bias4, y00, y01, y10, y11);
+        _Float16* sw = stg + P * SBUF + sw0;
+        *reinterpret_cast<h4*>(sw) = strip_act4<kActNone>(y00);
+        *reinterpret_cast<h4*>(sw + C) = strip_act4<kActNone>(y01);
+        *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<kActNone>(y10);
+        *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<kActNone>(y11);
+      }
+      lds_sync();
+    };
+    for (int it = begin; it < end;) {
+      decode(it);
+      const int len = min(end - it, a.tiles_h - j0);
+      lds_sync();  // the prologue
+      block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
+      it += len;
+    }
+    return;
+  }
+
+  // ---------------- load, transform and store waves ---------------------------
+  // Transform task (both transforms): tile tt, channel quad tq. Store task:
+  // 16-byte group sg of pixel sx in both rows of an output row pair.
+  const int gtid = tid - 512;
   const int tt = gtid >> 4;
   const int tq = gtid & 15;
-  // Row pair slots of phase k (from k6 = k % 6): the fold reads (k-1)%3 and
-  // k%3, the transform writes (k+1)%3.
-
-  // Store phase (conv1 waves): thread handles 16-byte group sg of pixel sx in
-  // both rows of the output row pair that left the conv2 fold last phase.
-  // The conv1 waves load the next row's residuals right after the store, or,
-  // in the ReLU / no-activation block with one residual input, after their
-  // fold, so that those registers are not live across it.
-  constexpr bool kSkipsAfterFold = ACT1 != kActSilu && NSKIP == 1;
   _Float16* const stg = blds + L::STG;
   const int sx = gtid >> 3;
   const int sg = gtid & 7;
@@ -252,7 +357,7 @@ winograd_block(BlockArgs a) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, n_rec, 0x00020000);
   };
   auto st_off = [&](bool live, int o, int r) -> uint32_t {
-    const bool ok = live && (r == 0 || 2 * o + 1 < a.H);  // uniform
+    const bool ok = live && (r == 0 || 2 * o + 1 < a.H);
     return ok ? lane_off + (uint32_t)r * rb32 : kOob;
   };
   auto load_skips = [&](bool live, int o) {
@@ -280,146 +385,36 @@ winograd_block(BlockArgs a) {
                                              kCachedOut ? 0 : kNonTemporal);
     }
   };
-  // U' of this wave: [dy][position][kc], 16 output channels.
-  auto load_u = [&](const uint16_t* packed, h8 (&u)[3][4][2]) {
-    const h8* up = reinterpret_cast<const h8*>(packed + L::UOFF) +
-                   (size_t)grp * (12 * 2 * 64) + lane;
+  _Float16* const vw1 = blds + L::V1 + StripLds<2>::at(tt, 4 * tq);
+  _Float16* const vw2 = blds + L::V2 + StripLds<2>::at(tt, 4 * tq);
+  // Input patch of t tile tt: padded columns pc0 .. pc0 + 3 with
+  // pc0 = 30 s - 1 + 2 tt, 8 bytes of channel quad tq each. The row goes in
+  // the instruction's scalar offset; columns outside the padded row get an
+  // out-of-range lane offset and rows outside the image a zero-size
+  // resource, both of which read as zero.
+  const int64_t img_bytes = (int64_t)a.Hp * row_bytes;
+  __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, 0, 0x00020000);
+  __amdgpu_buffer_rsrc_t rs0 = rs;
+  uint32_t col_off[4];
+  auto load2 = [&](h2 (&x)[16], int pr) {
 #pragma unroll
-    for (int dy = 0; dy < 3; ++dy)
+    for (int r = 0; r < 2; ++r) {
+      const bool row_ok = (pr + r >= 0) && (pr + r < a.Hp);
+      const __amdgpu_buffer_rsrc_t rr = row_ok ? rs : rs0;
+      const uint32_t ro = row_ok ? (uint32_t)(pr + r) * rb32 : 0u;
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int kc = 0; kc < 2; ++kc) u[dy][p][kc] = up[((dy * 4 + p) * 2 + kc) * 64];
+      for (int j = 0; j < 4; ++j) {
+        const h4 v =
+            __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rr, col_off[j], ro, 0));
+        x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
+        x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
+      }
+    }
   };
-  if (wave < 4) {
-    // ---------------- conv1: in -> t ----------------------------------------
-    h8 u[3][4][2];
-    load_u(a.u1, u);
-    const f4 bias4 = *reinterpret_cast<const f4*>(a.bias1 + ch0);
-    _Float16* const vw = blds + L::V1 + StripLds<2>::at(tt, 4 * tq);
-    const _Float16* vr[2];
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc) vr[kc] = blds + L::V1 + StripLds<2>::at(tcol, 32 * kc + 8 * kq);
-    _Float16* const ring = blds + L::RING;
-    // Ring offsets of this lane's four t values (pixel rows 0/1, columns
-    // 2 tcol / 2 tcol + 1, channel quad 4 grp + kq).
-    int rw[4];
-    {
-      const int q = 4 * grp + kq;
-      rw[0] = L::at(0, 2 * tcol, q);
-      rw[1] = L::at(0, 2 * tcol + 1, q);
-      rw[2] = L::at(1, 2 * tcol, q);
-      rw[3] = L::at(1, 2 * tcol + 1, q);
-    }
-    // Input patch of t tile tt: padded columns pc0 .. pc0 + 3 with
-    // pc0 = 30 s - 1 + 2 tt, 8 bytes of channel quad tq each. The row goes in
-    // the instruction's scalar offset; columns outside the padded row get an
-    // out-of-range lane offset and rows outside the image a zero-size
-    // resource, both of which read as zero.
-    const int64_t img_bytes = (int64_t)a.Hp * row_bytes;
-    __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, 0, 0x00020000);
-    __amdgpu_buffer_rsrc_t rs0 = rs;
-    uint32_t col_off[4];
-    auto load2 = [&](h2 (&x)[16], int pr) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const bool row_ok = (pr + r >= 0) && (pr + r < a.Hp);
-        const __amdgpu_buffer_rsrc_t rr = row_ok ? rs : rs0;
-        const uint32_t ro = row_ok ? (uint32_t)(pr + r) * rb32 : 0u;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h4 v = __builtin_bit_cast(
-              h4, __builtin_amdgcn_raw_buffer_load_b64(rr, col_off[j], ro, 0));
-          x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
-          x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
-        }
-      }
-    };
-    // Lane masks (all ones or zero) of this lane's two t columns, per run.
-    uint32_t cm0 = 0, cm1 = 0;
-    h2 X[16];  // input rows of the next row pair to transform
-    auto phase = [&](auto k6_tag, int k, int len) {
-      constexpr int K6 = decltype(k6_tag)::value;  // k % 6
-      constexpr int P = K6 & 1;
-      constexpr int SA = ((K6 + 2) % 3) * RPAIR, SB = (K6 % 3) * RPAIR, SW = ((K6 + 1) % 3) * RPAIR;
-      // Output row k-5 leaves staging (k-5)&1 = P^1 (the conv2 fold of the
-      // last phase); its residuals were loaded last phase. Then the residuals
-      // of row k-4 (folded by conv2 this phase, stored next phase).
-      store_row(k >= 5, j0 + k - 5, P ^ 1);
-      if constexpr (!kSkipsAfterFold) load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
-      if (k <= len) {
-        row_pair_transform(vw + SW, X);
-        // Q_{k+2}: padded rows 2 (j0 + k + 2) - 1 and 2 (j0 + k + 2).
-        load2(X, 2 * (j0 + k) + 3);
-      }
-      if (k >= 1 && k <= len + 1) {
-        // Fold t_{k-1}: t rows 2 (j0 + k - 1) - 1 + r, t columns 30 s - 1 + 2 tcol + dx.
-        f4 y00, y01, y10, y11;
-        block_fold(u, vr, SA, SB, bias4, y00, y01, y10, y11);
-        const int tr0 = 2 * (j0 + k - 1) - 1;
-        const uint32_t rm0 = (tr0 >= 0 && tr0 < a.H) ? ~0u : 0u;  // uniform
-        const uint32_t rm1 = (tr0 + 1 < a.H) ? ~0u : 0u;
-        // t outside the image is stored as zero (bitwise, so that no branch
-        // splits the phase).
-        auto masked = [&](f4 y, uint32_t m) {
-          u2 b = __builtin_bit_cast(u2, strip_act4<ACT1>(y));
-          b &= u2{m, m};
-          return b;
-        };
-        _Float16* sl = ring + (P ^ 1) * L::RSLOT;
-        *reinterpret_cast<u2*>(sl + rw[0]) = masked(y00, rm0 & cm0);
-        *reinterpret_cast<u2*>(sl + rw[1]) = masked(y01, rm0 & cm1);
-        *reinterpret_cast<u2*>(sl + rw[2]) = masked(y10, rm1 & cm0);
-        *reinterpret_cast<u2*>(sl + rw[3]) = masked(y11, rm1 & cm1);
-      }
-      if constexpr (kSkipsAfterFold) load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
-      lds_sync();
-    };
-    for (int it = begin; it < end;) {
-      decode(it);
-      const int len = min(end - it, a.tiles_h - j0);
-      {
-        const char* ib = reinterpret_cast<const char*>(a.in) + (int64_t)n * img_bytes;
-        rs = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, (int)img_bytes, 0x00020000);
-        rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, 0, 0x00020000);
-        const int pc0 = L::OPX * s - 1 + 2 * tt;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool ok = (pc0 + j >= 0) && (pc0 + j < a.Wp);
-          col_off[j] = ok ? (uint32_t)((pc0 + j) * PX + tq * 8) : kOob;
-        }
-        const int tc0 = L::OPX * s - 1 + 2 * tcol;
-        cm0 = (tc0 >= 0 && tc0 < a.W) ? ~0u : 0u;
-        cm1 = (tc0 + 1 < a.W) ? ~0u : 0u;
-        run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
-        lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
-      }
-      // Prologue: Q_0 (padded rows 2 j0 - 1, 2 j0) into V1 slot 0, then the
-      // rows of Q_1 for phase 0. Slot 0 is free: the last fold of an earlier
-      // run read it at least three barriers ago.
-      load2(X, 2 * j0 - 1);
-      row_pair_transform(vw, X);
-      load2(X, 2 * j0 + 1);
-      block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
-      it += len;
-    }
-    return;
-  }
-
-  // ---------------- conv2: t -> out ------------------------------------------
-  h8 u[3][4][2];
-  load_u(a.u2, u);
-  const f4 bias4 = *reinterpret_cast<const f4*>(a.bias2 + ch0);
-  _Float16* const vw = blds + L::V2 + StripLds<2>::at(tt, 4 * tq);
-  const _Float16* vr[2];
-#pragma unroll
-  for (int kc = 0; kc < 2; ++kc) vr[kc] = blds + L::V2 + StripLds<2>::at(tcol, 32 * kc + 8 * kq);
-  const _Float16* const ring = blds + L::RING;
   // Ring pixels of this task's patch: 2 tt .. 2 tt + 3 (tile 15 is not an
-  // output of the strip; it reads tile 14's patch).
-  // Row 0 addresses of the four pixels; row 1 and the slot are immediate
-  // offsets from them.
+  // output of the strip; it reads tile 14's patch). Row 0 addresses of the
+  // four pixels; row 1 and the slot are immediate offsets from them.
+  const _Float16* const ring = blds + L::RING;
   const _Float16* rp[4];
   {
     const int rx0 = 2 * (tt < L::OTILES ? tt : L::OTILES - 1);
@@ -436,34 +431,52 @@ winograd_block(BlockArgs a) {
         x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
       }
   };
-  const int sw0 = StripStage<2>::at(0, 2 * tcol, ch0 >> 3) + (ch0 & 7);
-  h2 T[16];
+  h2 X[16];  // input rows of the next row pair to transform
+  h2 T[16];  // the t rows read from the ring this phase
   auto phase = [&](auto k6_tag, int k, int len) {
     constexpr int K6 = decltype(k6_tag)::value;  // k % 6
     constexpr int P = K6 & 1;
-    constexpr int SA = ((K6 + 2) % 3) * RPAIR, SB = (K6 % 3) * RPAIR, SW = ((K6 + 1) % 3) * RPAIR;
-    // t_{k-2} from ring slot k&1, read at the start of the phase so that
-    // these LDS reads overlap the fold.
+    constexpr int SW = ((K6 + 1) % 3) * RPAIR;
+    // t_{k-2} from ring slot k&1, read first so that it lands during the
+    // store and the input transform.
     const bool tr = k >= 2 && k <= len + 2;
     if (tr) ring_load2(T, P);
-    const bool fold = k >= 4 && k <= len + 3;
-    if (fold) {
-      f4 y00, y01, y10, y11;
-      block_fold(u, vr, SA, SB, bias4, y00, y01, y10, y11);
-      _Float16* sw = stg + P * SBUF + sw0;
-      *reinterpret_cast<h4*>(sw) = strip_act4<kActNone>(y00);
-      *reinterpret_cast<h4*>(sw + C) = strip_act4<kActNone>(y01);
-      *reinterpret_cast<h4*>(sw + 32 * C) = strip_act4<kActNone>(y10);
-      *reinterpret_cast<h4*>(sw + 33 * C) = strip_act4<kActNone>(y11);
+    // Output row k-5 leaves staging (k-5)&1 = P^1 (the conv2 fold of the last
+    // phase) with the residuals loaded last phase; then the residuals of row
+    // k-4 (folded this phase, stored next phase).
+    store_row(k >= 5, j0 + k - 5, P ^ 1);
+    load_skips(k >= 4 && k <= len + 3, j0 + k - 4);
+    if (k <= len) {
+      row_pair_transform(vw1 + SW, X);
+      // Q_{k+2}: padded rows 2 (j0 + k + 2) - 1 and 2 (j0 + k + 2).
+      load2(X, 2 * (j0 + k) + 3);
     }
-    if (tr) row_pair_transform(vw + SW, T);
+    if (tr) row_pair_transform(vw2 + SW, T);
     lds_sync();
   };
   for (int it = begin; it < end;) {
     decode(it);
     const int len = min(end - it, a.tiles_h - j0);
-    run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
-    lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
+    {
+      const char* ib = reinterpret_cast<const char*>(a.in) + (int64_t)n * img_bytes;
+      rs = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, (int)img_bytes, 0x00020000);
+      rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, 0, 0x00020000);
+      const int pc0 = L::OPX * s - 1 + 2 * tt;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = (pc0 + j >= 0) && (pc0 + j < a.Wp);
+        col_off[j] = ok ? (uint32_t)((pc0 + j) * PX + tq * 8) : kOob;
+      }
+      run_pix = ((int64_t)n * a.Hp + 2 * j0 + 1) * a.Wp + L::OPX * s + 1;
+      lane_off = (sx < L::OPX && L::OPX * s + sx < a.W) ? s_lane : kOob;
+    }
+    // Prologue: Q_0 (padded rows 2 j0 - 1, 2 j0) into V1 slot 0, then the
+    // rows of Q_1 for phase 0. Slot 0 is free: the last fold of an earlier
+    // run read it at least three barriers ago.
+    load2(X, 2 * j0 - 1);
+    row_pair_transform(vw1, X);
+    load2(X, 2 * j0 + 1);
+    lds_sync();  // every role: the prologue's barrier
     block_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
     it += len;
   }
@@ -525,10 +538,10 @@ hipError_t launch_block(BlockArgs a, hipStream_t s) {
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  int64_t grid = cu_count();  // one 512-thread workgroup per CU (all of its LDS)
+  int64_t grid = cu_count();  // one workgroup per CU (12 waves, 128 KB of LDS)
   if (grid > items) grid = items;
   grid = (grid + 7) / 8 * 8;
-  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(512), lds, s, a);
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(BlockL::THREADS), lds, s, a);
   return hipGetLastError();
 }
 
