@@ -15,7 +15,8 @@ Extra objects in the line:
                 without them); per kernel: algorithmic bytes (each tensor the
                 launch reads or writes, fp16, once, plus weights) and algorithmic
                 flops (direct-conv equivalent, 2*9*Cin*Cout per pixel and conv, and
-                the Winograd-executed 16/36 of that) over the mean launch time.
+                the share a Winograd kernel executes: 16/36 for F(2x2,3x3), 6/9 for
+                the fused block's F(2,3) along x) over the mean launch time.
                 The bound follows the kernel's algorithmic intensity against the
                 MI355X ridge (2.5 PFLOP/s fp16 dense / 8 TB/s = 312 flop/B): a
                 fused block does 2 convs' flops per input/output pass (384
@@ -384,7 +385,9 @@ def launch_work(spec, steps, px: int):
             ci += 2
             b = 2.0 * px * (c1 + m2 * (1 + nsk)) + 18.0 * (c1 * m1 + c2 * m2)
             fd = 2.0 * 9 * px * (c1 * m1 + c2 * m2)
-            out.append({"bytes": b, "flops_direct": fd, "flops_wino": fd * 16 / 36, "convs": 2})
+            # The fused block runs F(2,3) along x, the kernel rows direct: 6 of
+            # the 9 products per output and channel pair.
+            out.append({"bytes": b, "flops_direct": fd, "flops_wino": fd * 6 / 9, "convs": 2})
         elif name.startswith(("winograd_conv", "direct_conv")):
             (c, m), nsk = convs[ci]
             ci += 1
