@@ -2692,6 +2692,8 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
   const int io = (w.in_nchw ? 1 : 0) | (w.epi.out_kind == kOutNchwF16 ? 2 : 0);
   if (io != 0) {
     if (!pipe_boundary_eligible(w)) return hipErrorInvalidValue;
+    if (rowpipe_eligible(64, 64, 0, w.epi.act, w.N, w.H, w.W, io))
+      return launch_rowpipe(a, w.epi.act, io, s);
     switch (io) {
       case 1: return launch_pipe<2, 0, 1>(a, w.epi.act, s);
       case 2: return launch_pipe<2, 0, 2>(a, w.epi.act, s);
@@ -2700,7 +2702,11 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
   }
   // 64 channels with residual inputs stay on winograd_strip (it runs at the
   // streaming rate there).
-  if (nskip == 0 && kc == 2) return launch_pipe<2, 0>(a, w.epi.act, s);
+  if (nskip == 0 && kc == 2) {
+    if (rowpipe_eligible(64, 64, 0, w.epi.act, w.N, w.H, w.W, 0))
+      return launch_rowpipe(a, w.epi.act, 0, s);
+    return launch_pipe<2, 0>(a, w.epi.act, s);
+  }
   if (kc == 3) {
     switch (nskip) {
       case 0: return launch_pipe<3, 0>(a, w.epi.act, s);

@@ -29,6 +29,13 @@ hipError_t launch_direct(DirectArgs a, hipStream_t s);
 // geometry runs fused; launch_block refuses what it does not accept.
 bool block_eligible(int C, int M, int act1, int act2, int64_t N, int64_t H, int64_t W);
 hipError_t launch_block(BlockArgs a, hipStream_t s);
+// A lone 64 -> 64 conv (bias, activation, no residual input) on the
+// row-Winograd pipe (rowpipe.hip): padded NHWC fp16 in and out, or the NCHW
+// fp16 boundary layout on the input (io bit 0) and / or output (io bit 1)
+// side; rowpipe_eligible says whether it takes the shape.
+bool rowpipe_eligible(int C, int M, int nskip, int act, int64_t N, int64_t H, int64_t W,
+                      int io);
+hipError_t launch_rowpipe(StripArgs a, int act, int io, hipStream_t s);
 hipError_t launch_eltwise(EltArgs a, bool binary, hipStream_t s);
 hipError_t launch_dts(DtsArgs a, hipStream_t s);
 hipError_t launch_input_convert(IoArgs a, hipStream_t s);

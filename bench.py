@@ -393,8 +393,10 @@ def launch_work(spec, steps, px: int):
             ci += 1
             b = 2.0 * px * (c + m * (1 + nsk)) + 18.0 * c * m
             fd = 2.0 * 9 * px * c * m
-            out.append({"bytes": b, "flops_direct": fd,
-                        "flops_wino": fd * 16 / 36 if c > 1 else fd, "convs": 1})
+            # A lone 64 -> 64 conv without residual inputs runs the fused
+            # block's row scheme (6/9 of direct); other convs F(2x2,3x3) (16/36).
+            fw = fd if c == 1 else fd * 6 / 9 if (c == m == 64 and nsk == 0) else fd * 16 / 36
+            out.append({"bytes": b, "flops_direct": fd, "flops_wino": fw, "convs": 1})
         else:
             out.append(None)
     return out
