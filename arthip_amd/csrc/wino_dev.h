@@ -140,23 +140,38 @@ __device__ __forceinline__ void strip_transform(_Float16* vw, const h2 (&top)[16
 // reciprocal, and x times it. Both products are FMAs with a zero addend, which
 // take x in fp16 directly (v_fma_mix_f32), so x is never converted on its own;
 // the values equal plain products except that a zero result is +0.
+// kInterleave writes the four chains stage by stage (four exps, four
+// reciprocals, four products), which the compiler then issues side by side;
+// written per element, it runs them one after another, each waiting on its
+// transcendentals. The arithmetic is the same either way.
+template <bool kInterleave = true>
 __device__ __forceinline__ h4 silu4(h4 r) {
-  f4 t;
+  f4 q, t;
+  if constexpr (kInterleave) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float x = (float)r[e];
-    const float q = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(x, -1.44269502f, 0.0f)));
-    t[e] = __builtin_fmaf(x, q, 0.0f);
+    for (int e = 0; e < 4; ++e)
+      q[e] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)r[e], -1.44269502f, 0.0f));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = __builtin_amdgcn_rcpf(1.0f + q[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = __builtin_fmaf((float)r[e], q[e], 0.0f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float x = (float)r[e];
+      q[e] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(x, -1.44269502f, 0.0f)));
+      t[e] = __builtin_fmaf(x, q[e], 0.0f);
+    }
   }
   return __builtin_convertvector(t, h4);
 }
 
 // fp16 rounding and activation of 4 channels whose accumulator holds the bias.
-template <int ACT>
+template <int ACT, bool kInterleave = true>
 __device__ __forceinline__ h4 strip_act4(f4 y) {
   h4 r = to_h4(y);
   if (ACT == kActRelu) r = __builtin_elementwise_max(r, h4{0, 0, 0, 0});
-  if (ACT == kActSilu) r = silu4(r);
+  if (ACT == kActSilu) r = silu4<kInterleave>(r);
   return r;
 }
 
