@@ -281,6 +281,15 @@ def test_pipe_silu_c64(h, w):
     check(run_conv(x, wt, b, 2), oracle_conv(x, wt, b, 2), f"pipe64 silu {h}x{w}")
 
 
+# A lone 64 -> 64 conv runs the row-Winograd pipe (64-pixel strips): a batch
+# of two with a partial last strip and an odd height, so that workgroup runs
+# cross strip and image boundaries, each activation.
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_rowpipe_batch_runs(act):
+    x, wt, b = make_case(41, 2, 64, 64, 271, 200)
+    check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"rowpipe batch2 271x200 act{act}")
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 def test_pipe_epilogue_c96(act):
     x, wt, b = make_case(32, 1, 96, 96, 21, 70)

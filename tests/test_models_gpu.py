@@ -10,7 +10,8 @@ Gates:
 - max-abs <= 2e-2 and PSNR >= 50 dB (peak 1) where the configuration's output
   range allows it (C4F32, the single layer, the shipped luma model); the
   shipped model is also held to max-abs <= 1.34e-3, the reference's accuracy
-  against ONNX Runtime CPU at 1920x1080 (NOTES.md:78-79);
+  against ONNX Runtime CPU at 1920x1080 (NOTES.md:78-79), with at most four of
+  the 1920x1080 frame's 8.3 M samples one fp16 ulp past it;
 - for the deep He-normal models the fp16-storage floor of the model itself is
   far above that (outputs span ~+-200), so those are gated on relative RMS
   error <= 3x the floor measured in the same test (the engine measures ~2x).
@@ -615,3 +616,21 @@ def test_pipe_nchw_boundary(act, hw):
         want = run_model(model, x)
         s = _compare(got.astype(np.float32), want)
         assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
+
+
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_pipe_nchw_boundary_batch(act):
+    """The NCHW boundary conv on a batch of two (each image's planes at its own
+    offset, workgroup runs crossing strips and images): bit for bit the padded
+    path, and the literal gate against the oracle."""
+    from tests.test_conv_kernel_gpu import run_conv
+    model, w16, b16 = _conv64(act)
+    x = models.synthetic_input((2, 64, 37, 136), seed=5, kind="normal")
+    with Engine(0) as e:
+        got, names = _steps(e.build(model), x)
+    assert not any(n.startswith(("input_convert", "output_convert")) for n in names), names
+    code = {None: 0, "silu": 2}[act]
+    ref = run_conv(x, w16, b16, act=code)
+    np.testing.assert_array_equal(got.view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    s = _compare(got.astype(np.float32), run_model(model, x))
+    assert s["max_abs"] <= 2e-2 and s["psnr"] >= 50.0, s
