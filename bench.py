@@ -311,11 +311,13 @@ def host_path(args) -> int:
     return 0
 
 
-def end_to_end(spec, eng, x_host, frames: int) -> dict:
+def end_to_end(spec, eng, x_host, frames: int, vs_frames: int) -> dict:
     """Frame rates with host buffers (PCIe included), beside the device-resident
     value: the engine's own Run (pinned staging, upload, run, download, one
     engine, synchronous) and the VapourSynth filter path with two engines and
-    three caller threads (transfers of one frame overlap another's run)."""
+    three caller threads (transfers of one frame overlap another's run; timed
+    over vs_frames after 20 warm-up frames, since a new filter's first frames
+    run slower)."""
     t0 = time.perf_counter()
     for _ in range(frames):
         eng.run(x_host)
@@ -324,10 +326,10 @@ def end_to_end(spec, eng, x_host, frames: int) -> dict:
     out = {"engine_run_fps": round(n * sync_fps, 3),
            "engine_run_what": f"arthip_engine_run host->host, one engine, {frames} frames"}
     if spec.in_channels == 1 and n == 1:
-        wall = host_path_wall(spec, h, w, 2, 3, frames)
-        out["vs_filter_fps"] = round(frames / wall, 3)
+        wall = host_path_wall(spec, h, w, 2, 20, vs_frames)
+        out["vs_filter_fps"] = round(vs_frames / wall, 3)
         out["vs_filter_what"] = (f"VapourSynth filter core (GRAYH planes in host memory), "
-                                 f"num_streams=2, 3 caller threads, {frames} frames")
+                                 f"num_streams=2, 3 caller threads, {vs_frames} frames")
     return out
 
 
@@ -720,7 +722,8 @@ def main() -> int:
             }
 
     # Host-buffer rates (PCIe included): reported beside the device-resident value.
-    e2e = end_to_end(spec, eng, x_host, max(4, min(args.steps, 40))) if not args.no_e2e else None
+    e2e = (end_to_end(spec, eng, x_host, max(4, min(args.steps, 40)), max(4, min(2 * args.steps, 200)))
+           if not args.no_e2e else None)
 
     rows = args.cpu_rows
     if rows < 0:
