@@ -423,12 +423,18 @@ winograd_block(BlockArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) rp[j] = ring + L::at(0, rx0 + j, tq);
   }
+  // Tile 15 is folded by conv2 (the MFMA takes 16 tiles) but never stored: its
+  // transformed input is zero, which the matrix units multiply at less power
+  // than a copy of tile 14.
+  const uint32_t tmask = tt < L::OTILES ? ~0u : 0u;
   auto ring_load2 = [&](h2 (&x)[16], int sl) {
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const h4 v = *reinterpret_cast<const h4*>(rp[j] + sl * L::RSLOT + r * 32 * C);
+        u2 b = *reinterpret_cast<const u2*>(rp[j] + sl * L::RSLOT + r * 32 * C);
+        b &= u2{tmask, tmask};
+        const h4 v = __builtin_bit_cast(h4, b);
         x[2 * (4 * r + j)] = __builtin_shufflevector(v, v, 0, 1);
         x[2 * (4 * r + j) + 1] = __builtin_shufflevector(v, v, 2, 3);
       }
