@@ -20,8 +20,8 @@ namespace arthip {
 //
 // Items are one output tile row (two pixel rows) x 32 tiles (64 pixels),
 // ordered (image, 64-pixel strip, tile row) with the tile row fastest; one
-// 768-thread workgroup per CU (12 waves, three per SIMD, 128 KB of LDS) walks
-// runs of them down a strip.
+// 768-thread workgroup per CU (12 waves, three per SIMD, 128 KB of LDS, up to
+// 152 KB with the boundary layouts) walks runs of them down a strip.
 //   waves 0-7  fold: wave w holds U' of output channels 16 (w & 3) .. + 15
 //              (96 VGPRs, the packed row filters) and folds the 16 tiles
 //              16 (w >> 2) .. + 15 of each item into staging, with bias and
@@ -40,9 +40,8 @@ namespace arthip {
 //   load waves:  store item k-2 from staging[(k-1)&1] (k >= 2); transform
 //                Q_{k+1} into slot (k+1)%3 and load the rows of Q_{k+2}
 //                (k < len)
-// The fold is block_fold's (row_pair_transform's V, chains X / b / P / c); the
-// per-element arithmetic equals the fused block's, so results match a
-// separate launch of the block's conv1 at even tile offsets.
+// The fold is block_fold's (row_pair_transform's V, chains X / b / P / c): the
+// fused block's per-element arithmetic, here on tiles at even columns.
 //
 // Boundary layouts (IO bit 0: NCHW input, bit 1: NCHW output; W % 8 == 0), the
 // same arithmetic in other layouts:
