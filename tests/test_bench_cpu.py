@@ -50,3 +50,27 @@ def test_launch_work_counts_each_distinct_tensor_once():
     got = [x["bytes"] for x in bench.launch_work(sh, steps, px)]
     assert got[2] == 3 * act + w2
     assert got[1] == 2 * act + 18.0 * 64 * 64
+
+
+def test_end_to_end_reports_a_failed_filter_child(monkeypatch):
+    """The VapourSynth-path rate runs in a child process; if the child fails,
+    the bench line carries null and the error instead of failing as a whole."""
+    import subprocess
+
+    class Res:
+        returncode = 1
+        stdout = ""
+        stderr = "no device"
+
+    class Spec:
+        in_channels = 1
+        name = "r8f64"
+
+    class Eng:
+        def run(self, x):
+            return x
+
+    monkeypatch.setattr(subprocess, "run", lambda *a, **k: Res())
+    out = bench.end_to_end(Spec(), Eng(), np.zeros((1, 1, 8, 8), np.float16), 2, 4)
+    assert out["vs_filter_fps"] is None
+    assert "exit 1" in out["vs_filter_error"] and "no device" in out["vs_filter_error"]
