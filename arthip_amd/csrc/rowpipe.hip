@@ -117,6 +117,33 @@ __device__ __forceinline__ void rp_transform(_Float16* vw, const h2 (&x)[16]) {
   }
 }
 
+// The same transform for one tile and one channel octet (element 4 r + j of
+// x: row r, column j, channels 8 g .. 8 g + 7), written as 16-byte groups.
+__device__ __forceinline__ void rp_transform8(_Float16* vw, const h8 (&x)[8]) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    h2 o[4][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const h2 d0 = h2{x[4 * r][2 * e], x[4 * r][2 * e + 1]};
+      const h2 d1 = h2{x[4 * r + 1][2 * e], x[4 * r + 1][2 * e + 1]};
+      const h2 d2 = h2{x[4 * r + 2][2 * e], x[4 * r + 2][2 * e + 1]};
+      const h2 d3 = h2{x[4 * r + 3][2 * e], x[4 * r + 3][2 * e + 1]};
+      o[0][e] = pk_sub(d0, d2);
+      o[1][e] = d1 + d2;
+      o[2][e] = pk_sub(d2, d1);
+      o[3][e] = pk_sub(d3, d1);
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const h4 lo = __builtin_shufflevector(o[p][0], o[p][1], 0, 1, 2, 3);
+      const h4 hi = __builtin_shufflevector(o[p][2], o[p][3], 0, 1, 2, 3);
+      *reinterpret_cast<h8*>(vw + r * RowPipeL::RROW + p * RowPipeL::WPS) =
+          __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  }
+}
+
 // Fold of one item half (16 tiles, two output rows) x 16 output channels from
 // row pairs A (rows R0, R1) and B (R2, R3): the fused block's chains.
 __device__ __forceinline__ void rp_fold(const h8 (&u)[3][4][2], const _Float16* const (&vr)[2],
@@ -273,42 +300,43 @@ winograd_rowpipe(StripArgs a) {
   }
 
   // ---------------- load, transform and store waves ---------------------------
-  // Transform tasks: tiles tt and tt + 16, channel quad tq (padded input:
-  // tt = gtid / 16; NCHW input: channel quads by wave). Store tasks (padded
+  // Transform tasks. Padded input: tile t8 and channel octet g8 per thread,
+  // t8 = 8 pw + 2 ((l >> 3) & 3) + (l >> 5), so that lanes l and l + 32,
+  // whose 16-byte writes the LDS serves together, take tiles of opposite
+  // parity (their two 128-byte tile rows cover all 64 banks). NCHW input:
+  // tiles tt and tt + 16, channel quad tq by wave. Store tasks (padded
   // output): 16-byte group sg of pixels sx and sx + 32 in both rows of an item.
   const int gtid = tid - 512;
   const int pw = wave - 8;
-  const int tt = IN_NCHW ? (lane & 15) : (gtid >> 4);
-  const int tq = IN_NCHW ? 4 * pw + (lane >> 4) : (gtid & 15);
+  const int tt = lane & 15;
+  const int tq = 4 * pw + (lane >> 4);
+  const int t8 = 8 * pw + 2 * ((lane >> 3) & 3) + (lane >> 5);
+  const int g8 = lane & 7;
   const int sx = gtid >> 3;
   const int sg = gtid & 7;
   _Float16* vw[2];
   vw[0] = plds + L::V + L::at(tt, 4 * tq);
   vw[1] = plds + L::V + L::at(tt + 16, 4 * tq);
+  _Float16* const vw8 = plds + L::V + L::at(t8, 8 * g8);
   const uint32_t plane = (uint32_t)a.H * (uint32_t)a.W * 2;  // NCHW channel plane bytes
-  // Input patch of tile tt (+ 16 v): padded columns pc0 .. pc0 + 3 with
-  // pc0 = 64 s + 2 (tt + 16 v), 8 bytes of channel quad tq each; the row in the
-  // scalar offset. Columns past the padded row get an out-of-range lane offset
-  // and rows past the image a zero-size resource (both read as zero).
+  // Input patch of tile t8: padded columns pc0 .. pc0 + 3 with pc0 = 64 s +
+  // 2 t8, 16 bytes of channel octet g8 each; the row in the scalar offset.
+  // Columns past the padded row get an out-of-range lane offset and rows past
+  // the image a zero-size resource (both read as zero).
   const int64_t img_bytes = (int64_t)a.Hp * row_bytes;
   __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, 0, 0x00020000);
   __amdgpu_buffer_rsrc_t rs0 = rs;
-  uint32_t col_off[2][4];
-  auto load2 = [&](h2 (&x)[2][16], int pr) {
+  uint32_t col_off[4];
+  auto load8 = [&](h8 (&x)[8], int pr) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const bool row_ok = pr + r < a.Hp;  // uniform
       const __amdgpu_buffer_rsrc_t rr = row_ok ? rs : rs0;
       const uint32_t ro = row_ok ? (uint32_t)(pr + r) * rb32 : 0u;
 #pragma unroll
-      for (int v = 0; v < 2; ++v)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const h4 q = __builtin_bit_cast(
-              h4, __builtin_amdgcn_raw_buffer_load_b64(rr, col_off[v][j], ro, 0));
-          x[v][2 * (4 * r + j)] = __builtin_shufflevector(q, q, 0, 1);
-          x[v][2 * (4 * r + j) + 1] = __builtin_shufflevector(q, q, 2, 3);
-        }
+      for (int j = 0; j < 4; ++j)
+        x[4 * r + j] =
+            __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rr, col_off[j], ro, 0));
     }
   };
   // NCHW input ring of this wave: the five 16-byte copies of lane l are
@@ -423,7 +451,8 @@ winograd_rowpipe(StripArgs a) {
       }
     }
   };
-  h2 X[2][16];
+  h2 X[2][16];  // NCHW input: tiles tt, tt + 16
+  h8 X8[8];      // padded input: tile t8
   auto phase = [&](auto k6_tag, int k, int len) {
     constexpr int K6 = decltype(k6_tag)::value;  // k % 6
     constexpr int P = K6 & 1;
@@ -441,10 +470,13 @@ winograd_rowpipe(StripArgs a) {
     // put it.
     store_item(k >= 2, k - 2, P ^ 1);
     if (k < len) {
+      if constexpr (IN_NCHW) {
 #pragma unroll
-      for (int v = 0; v < 2; ++v) rp_transform(vw[v] + SW, X[v]);
-      // Q_{k+2}: padded rows 2 (j0 + k + 2) and + 1.
-      if constexpr (!IN_NCHW) load2(X, 2 * (j0 + k) + 4);
+        for (int v = 0; v < 2; ++v) rp_transform(vw[v] + SW, X[v]);
+      } else {
+        rp_transform8(vw8 + SW, X8);
+        load8(X8, 2 * (j0 + k) + 4);  // Q_{k+2}: padded rows 2 (j0 + k + 2) and + 1
+      }
     }
     lds_sync();
   };
@@ -459,13 +491,10 @@ winograd_rowpipe(StripArgs a) {
       const char* ib = reinterpret_cast<const char*>(a.in) + (int64_t)n * img_bytes;
       rs = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, (int)img_bytes, 0x00020000);
       rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)ib, (short)0, 0, 0x00020000);
+      const int pc0 = L::OPX * s + 2 * t8;
 #pragma unroll
-      for (int v = 0; v < 2; ++v) {
-        const int pc0 = L::OPX * s + 2 * (tt + 16 * v);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          col_off[v][j] = (pc0 + j < a.Wp) ? (uint32_t)((pc0 + j) * PX + tq * 8) : kOob;
-      }
+      for (int j = 0; j < 4; ++j)
+        col_off[j] = (pc0 + j < a.Wp) ? (uint32_t)((pc0 + j) * PX + g8 * 16) : kOob;
     }
     if constexpr (OUT_NCHW) {
       out_img = reinterpret_cast<const char*>(a.out) + (int64_t)n * C * plane;
@@ -490,12 +519,13 @@ winograd_rowpipe(StripArgs a) {
       wait_vmcnt<0>();
       read_ring(X);
       issue(1);
-    } else {
-      load2(X, 2 * j0);
-    }
 #pragma unroll
-    for (int v = 0; v < 2; ++v) rp_transform(vw[v], X[v]);
-    if constexpr (!IN_NCHW) load2(X, 2 * j0 + 2);
+      for (int v = 0; v < 2; ++v) rp_transform(vw[v], X[v]);
+    } else {
+      load8(X8, 2 * j0);
+      rp_transform8(vw8, X8);
+      load8(X8, 2 * j0 + 2);
+    }
     lds_sync();
     rp_phases(len, [&](auto pt, int k) { phase(pt, k, len); });
     it += len;
