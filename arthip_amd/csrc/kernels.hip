@@ -2708,6 +2708,10 @@ hipError_t launch_strip(const WinoArgs& w, hipStream_t s) {
     return launch_pipe<2, 0>(a, w.epi.act, s);
   }
   if (kc == 3) {
+    // Up to one residual input the row pipe; with two the pipe, whose deeper
+    // row lookahead keeps more of the residual reads in flight.
+    if (rowpipe96_eligible(w.C, w.M, nskip, w.epi.act, w.N, w.H, w.W, 0))
+      return launch_rowpipe96(a, w.epi.act, s);
     switch (nskip) {
       case 0: return launch_pipe<3, 0>(a, w.epi.act, s);
       case 1: return launch_pipe<3, 1>(a, w.epi.act, s);

@@ -36,6 +36,12 @@ hipError_t launch_block(BlockArgs a, hipStream_t s);
 bool rowpipe_eligible(int C, int M, int nskip, int act, int64_t N, int64_t H, int64_t W,
                       int io);
 hipError_t launch_rowpipe(StripArgs a, int act, int io, hipStream_t s);
+// A lone 96 -> 96 conv (bias, activation, at most one residual input; padded
+// NHWC fp16 in and out) on the row-Winograd pipe (rowpipe96.hip);
+// rowpipe96_eligible says whether it takes the shape.
+bool rowpipe96_eligible(int C, int M, int nskip, int act, int64_t N, int64_t H, int64_t W,
+                        int io);
+hipError_t launch_rowpipe96(StripArgs a, int act, hipStream_t s);
 hipError_t launch_eltwise(EltArgs a, bool binary, hipStream_t s);
 hipError_t launch_dts(DtsArgs a, hipStream_t s);
 hipError_t launch_input_convert(IoArgs a, hipStream_t s);

@@ -21,7 +21,8 @@ size_t winograd_u_halfs(int C, int M) {
 }
 
 size_t block_u_halfs(int C, int M) {
-  return (C == 64 && M == 64) ? static_cast<size_t>(M / 16) * 12 * (C / 32) * 64 * 8 : 0;
+  const bool rows = C == M && (C == 64 || C == 96);
+  return rows ? static_cast<size_t>(M / 16) * 12 * (C / 32) * 64 * 8 : 0;
 }
 
 size_t block_u_offset(int C, int M) { return winograd_u_halfs(C, M) + narrow_packed_halfs(C, M); }

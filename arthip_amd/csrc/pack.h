@@ -36,14 +36,14 @@ size_t narrow_packed_halfs(int C, int M);
 
 // Halfs in the packed buffer: U' as [n_ob][16 positions][kc][64 lanes][8],
 // followed by the narrow taps when narrow_eligible(C, M), followed for
-// C = M = 64 by the row-Winograd filters of the fused residual block
-// (block_u_halfs).
+// C = M = 64 and C = M = 96 by the row-Winograd filters (block_u_halfs).
 size_t winograd_packed_halfs(int C, int M);
-// The fused residual block (C = M = 64) runs F(2,3) along x and sums the three
-// kernel rows in the MFMA: per kernel row dy the 1-D transform
-// U_dy = G (w[dy][0], w[dy][1], w[dy][2]) (G as above, unscaled), packed as
-// [n_ob][3 dy][4 positions][kc][64 lanes][8] in MFMA A-operand order. Its
-// offset in the packed buffer is block_u_offset(C, M); 0 halfs for other shapes.
+// The row-Winograd kernels (the fused residual block and the row pipes,
+// C = M = 64 or 96) run F(2,3) along x and sum the three kernel rows in the
+// MFMA: per kernel row dy the 1-D transform U_dy = G (w[dy][0], w[dy][1],
+// w[dy][2]) (G as above, unscaled), packed as [n_ob][3 dy][4 positions][kc]
+// [64 lanes][8] in MFMA A-operand order. Its offset in the packed buffer is
+// block_u_offset(C, M); 0 halfs for other shapes.
 size_t block_u_halfs(int C, int M);
 size_t block_u_offset(int C, int M);
 // Halfs of the U' part alone (offset of the narrow taps).

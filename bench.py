@@ -411,9 +411,11 @@ def launch_work(spec, steps, px: int):
             ci += 1
             b = 2.0 * px * (c + m * (1 + nsk)) + 18.0 * c * m
             fd = 2.0 * 9 * px * c * m
-            # A lone 64 -> 64 conv without residual inputs runs the fused
-            # block's row scheme (6/9 of direct); other convs F(2x2,3x3) (16/36).
-            fw = fd if c == 1 else fd * 6 / 9 if (c == m == 64 and nsk == 0) else fd * 16 / 36
+            # The row pipes run the fused block's row scheme (6/9 of direct): a
+            # lone 64 -> 64 conv without residual inputs, a 96 -> 96 conv with
+            # at most one. Other convs F(2x2,3x3) (16/36).
+            rows = (c == m == 64 and nsk == 0) or (c == m == 96 and nsk <= 1)
+            fw = fd if c == 1 else fd * 6 / 9 if rows else fd * 16 / 36
             out.append({"bytes": b, "flops_direct": fd, "flops_wino": fw, "convs": 1})
         else:
             out.append(None)

@@ -72,8 +72,9 @@ def test_winograd_pack_layout():
         kc = (c_in + 31) // 32
         n_ob = (m_out + 15) // 16
         n_wino = n_ob * 16 * kc * 64 * 8
-        # 64 -> 64 also carries the fused block's row filters after U'.
-        assert n_u == n_wino + (n_ob * 12 * kc * 64 * 8 if (c_in, m_out) == (64, 64) else 0)
+        # 64 -> 64 and 96 -> 96 also carry the row-Winograd filters after U'.
+        rows = (c_in, m_out) in ((64, 64), (96, 96))
+        assert n_u == n_wino + (n_ob * 12 * kc * 64 * 8 if rows else 0)
         up = u[:n_wino].view(np.float16).reshape(n_ob, 16, kc, 64, 8).astype(np.float64)
         for m in range(m_out):
             for c in range(c_in):
@@ -97,28 +98,33 @@ def test_winograd_pack_layout():
 G_ROW = np.array([[1, 0, 0], [0.5, 0.5, 0.5], [0.5, -0.5, 0.5], [0, 0, 1]])
 
 
-def _packed_64(w):
+def _packed_rows(w):
+    """The row filters of a C -> C conv (C = 64 or 96) as [ob][dy][p][kc][lane][e]."""
+    ch = w.shape[0]
     lib = _lib.lib()
-    n_u = lib.arthip_conv3x3_packed_halfs(64, 64)
+    n_u = lib.arthip_conv3x3_packed_halfs(ch, ch)
     u = np.zeros(n_u, np.uint16)
-    b = np.zeros(lib.arthip_conv3x3_bias_len(64), np.float32)
+    b = np.zeros(lib.arthip_conv3x3_bias_len(ch), np.float32)
     rc = lib.arthip_conv3x3_pack(
-        w.view(np.uint16).ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), None, 64, 64,
+        w.view(np.uint16).ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), None, ch, ch,
         u.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), n_u,
         b.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), b.size)
     assert rc == 0
-    return u[4 * 16 * 2 * 64 * 8:].view(np.float16).reshape(4, 3, 4, 2, 64, 8).astype(np.float64)
+    n_ob, kc = ch // 16, ch // 32
+    return u[n_ob * 16 * kc * 64 * 8:].view(np.float16).reshape(
+        n_ob, 3, 4, kc, 64, 8).astype(np.float64)
 
 
-def test_block_row_filter_layout():
-    """The fused block's row filters after U' of a 64 -> 64 conv:
+@pytest.mark.parametrize("ch", [64, 96])
+def test_block_row_filter_layout(ch):
+    """The row-Winograd filters after U' of a 64 -> 64 or 96 -> 96 conv:
     [ob][dy][p][kc][lane][e] = fp16(G[p] . w[m][c][dy][:]) with m = 16*ob + lane % 16 and
     c = 32*kc + 8*(lane // 16) + e."""
-    w = (np.random.default_rng(8).standard_normal((64, 64, 3, 3)) * 0.2).astype(np.float16)
-    up = _packed_64(w)
+    w = (np.random.default_rng(8).standard_normal((ch, ch, 3, 3)) * 0.2).astype(np.float16)
+    up = _packed_rows(w)
     want = np.einsum("pj,mcyj->mcyp", G_ROW, w.astype(np.float64)).astype(np.float16)
-    m = np.arange(64)[:, None]
-    c = np.arange(64)[None, :]
+    m = np.arange(ch)[:, None]
+    c = np.arange(ch)[None, :]
     ob, row = m // 16, m % 16
     kc, kk = c // 32, c % 32
     lane, e = row + 16 * (kk // 8), kk % 8
@@ -137,7 +143,7 @@ def test_block_row_winograd_reproduces_the_conv():
     filters as packed in fp16). A planted sign error in V3 or in the fold fails."""
     rng = np.random.default_rng(9)
     w = (rng.standard_normal((64, 64, 3, 3)) * 0.2).astype(np.float16)
-    up = _packed_64(w)
+    up = _packed_rows(w)
     # U[m][c][dy][p] back from the A-operand layout.
     u = np.zeros((64, 64, 3, 4))
     m = np.arange(64)[:, None]
@@ -174,6 +180,41 @@ def test_block_row_winograd_reproduces_the_conv():
     assert np.abs(bad1 - y1).max() > 1e-2
     bad0, bad1 = fold(q_coef=2.0)
     assert np.abs(bad1 - y1).max() > 1e-2
+
+
+def test_row_pipe96_position_split_reproduces_the_conv():
+    """The 96-channel row pipe's arithmetic on the CPU, from the packed row
+    filters: one wave accumulates X = M2 and T = bias + M1, another P = M0 and
+    Q = M3 (V3 negated), and the outputs y0 = T + X + P and y1 = T - X + Q equal
+    the two outputs of a direct 3x3 correlation with the taps the rounded
+    filters imply (fp64). A planted sign error in the combination fails."""
+    rng = np.random.default_rng(10)
+    w = (rng.standard_normal((96, 96, 3, 3)) * 0.2).astype(np.float16)
+    up = _packed_rows(w)
+    u = np.zeros((96, 96, 3, 4))
+    m = np.arange(96)[:, None]
+    c = np.arange(96)[None, :]
+    lane, e = m % 16 + 16 * ((c % 32) // 8), (c % 32) % 8
+    for dy in range(3):
+        for p in range(4):
+            u[:, :, dy, p] = up[m // 16, dy, p, c // 32, lane, e]
+    d = rng.standard_normal((96, 3, 4))
+    bias = rng.standard_normal(96)
+    v = np.stack([d[..., 0] - d[..., 2], d[..., 1] + d[..., 2], d[..., 2] - d[..., 1],
+                  d[..., 3] - d[..., 1]], axis=-1)
+    mp = np.einsum("mcyp,cyp->mp", u, v)
+    x, t, pp, q = mp[:, 2], bias + mp[:, 1], mp[:, 0], mp[:, 3]
+    u0, u1, u2, u3 = (u[..., p] for p in range(4))
+    t0 = np.stack([u0, u1 - u2, u1 + u2 - u0], axis=-1)
+    t1 = np.stack([u1 + u2 - u3, u1 - u2, u3], axis=-1)
+    y0 = np.einsum("mcyx,cyx->m", t0, d[..., 0:3]) + bias
+    y1 = np.einsum("mcyx,cyx->m", t1, d[..., 1:4]) + bias
+    np.testing.assert_allclose(t + x + pp, y0, rtol=0, atol=1e-9)
+    np.testing.assert_allclose(t - x + q, y1, rtol=0, atol=1e-9)
+    assert np.abs(t + x - q - y1).max() > 1e-2
+    assert np.abs(t - x + pp - y0).max() > 1e-2
+    w64 = w.astype(np.float64)
+    assert np.abs(t0 - w64).max() < 4e-3 and np.abs(t1 - w64).max() < 4e-3
 
 
 def test_padded_dims():

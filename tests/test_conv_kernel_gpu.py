@@ -250,9 +250,10 @@ def test_head_mfma_epilogue_batch(act):
     check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"head act{act}")
 
 
-# C == M in {64, 96} without residual inputs runs the producer/consumer kernel
-# (winograd_pipe): the same strips, with the producers' row window restarting
-# at every strip boundary of a workgroup's item range.
+# C == M in {64, 96} without residual inputs runs a row-Winograd pipe
+# (winograd_rowpipe on 64-pixel strips at 64 channels, winograd_rowpipe96 on
+# 32-pixel strips at 96), its load waves' rows restarting at every strip
+# boundary of a workgroup's item range.
 @pytest.mark.parametrize("c", [64, 96])
 @pytest.mark.parametrize("h,w", GEOMETRY)
 def test_pipe_geometry(c, h, w):
@@ -290,6 +291,16 @@ def test_rowpipe_batch_runs(act):
     check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"rowpipe batch2 271x200 act{act}")
 
 
+# A lone 96 -> 96 conv without residual inputs runs winograd_rowpipe96
+# (32-pixel strips, the row filters split by position pairs over two waves):
+# a batch of two with a partial last strip and an odd height, so that
+# workgroup runs cross strip and image boundaries, each activation.
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_rowpipe96_batch_runs(act):
+    x, wt, b = make_case(42, 2, 96, 96, 137, 100)
+    check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"rowpipe96 batch2 137x100 act{act}")
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 def test_pipe_epilogue_c96(act):
     x, wt, b = make_case(32, 1, 96, 96, 21, 70)
@@ -310,8 +321,9 @@ def test_pipe_long_runs_c96():
 @pytest.mark.parametrize("nskip", [1, 2])
 @pytest.mark.parametrize("h,w", [(8, 17), (17, 33), (33, 17), (1082, 64), (54, 1920)])
 def test_pipe_residual_c96(nskip, h, w):
-    """96 channels with residual inputs: the producers load the residual chunks
-    into registers a step ahead and add them, in graph order, as they store."""
+    """96 channels with residual inputs (one: winograd_rowpipe96; two:
+    winograd_pipe): the load waves fetch the residual chunks into registers a
+    phase ahead and add them, in graph order, as they store."""
     x, wt, b = make_case(35, 1, 96, 96, h, w)
     rng = np.random.default_rng(36)
     skips = [rng.standard_normal((1, 96, h, w)).astype(np.float16) for _ in range(nskip)]
