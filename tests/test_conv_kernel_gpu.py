@@ -301,6 +301,16 @@ def test_rowpipe96_batch_runs(act):
     check(run_conv(x, wt, b, act), oracle_conv(x, wt, b, act), f"rowpipe96 batch2 137x100 act{act}")
 
 
+# winograd_rowpipe96 with one residual input, each activation (applied before
+# the residual add, which the load waves do in fp16 as they store).
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_rowpipe96_residual_epilogues(act):
+    x, wt, b = make_case(43, 1, 96, 96, 35, 70)
+    skip = [np.random.default_rng(44).standard_normal((1, 96, 35, 70)).astype(np.float16)]
+    check(run_conv(x, wt, b, act, skip), oracle_conv(x, wt, b, act, skip),
+          f"rowpipe96 skip1 act{act} 35x70")
+
+
 @pytest.mark.parametrize("act", [0, 1, 2])
 def test_pipe_epilogue_c96(act):
     x, wt, b = make_case(32, 1, 96, 96, 21, 70)
